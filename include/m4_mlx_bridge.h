@@ -1,0 +1,171 @@
+/*
+ * m4_mlx_bridge.h -- C-ABI of the MI355X quantization-router prefill path.
+ *
+ * Drop-in for the reference's core/bridge/m4_mlx_bridge.h:23-106: the same
+ * eight entry points with the same argument meaning, return values and
+ * validation order, exported from libm4_bridge.so.  Pointers are DEVICE
+ * pointers (hipMalloc / torch-ROCm data_ptr()); host pointers are accepted
+ * too and staged through device memory (slower, PCIe-bound).  Kernels run
+ * on the bridge stream (m4_bridge_set_stream) asynchronously;
+ * m4_bridge_synchronize() waits for everything issued so far.
+ *
+ * Error codes (checked in this order, before any device work,
+ * core/bridge/m4_mlx_bridge.mm:201-230):
+ *   -1 bridge not initialized
+ *   -2 null pointer, odd (non-2-byte-aligned) X or Y, or a buffer too small
+ *   -3 invalid format (the projection entry points accept ids 0..5)
+ *   -4 invalid dimension: M, K or N zero; K % 32; K % 256 for formats 2, 4, 5
+ *   -5 device staging allocation failed
+ *   -6 kernel launch / device failure
+ *
+ * The entry points below the first block have no single counterpart in the
+ * reference's C-ABI; each names the reference routine it replaces.
+ */
+#ifndef M4_MLX_BRIDGE_H
+#define M4_MLX_BRIDGE_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define M4_API __attribute__((visibility("default")))
+#else
+#define M4_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference C-ABI (core/bridge/m4_mlx_bridge.h) ---------------------- */
+
+/* m4_mlx_bridge.h:23 -- selects the HIP device, creates the bridge stream.
+ * The path argument is accepted for compatibility and ignored (kernels are
+ * compiled into the library). */
+M4_API bool m4_bridge_init(const char* metallib_path);
+
+/* m4_mlx_bridge.h:33 -- minimum W bytes for format 0..5, else 0. */
+M4_API size_t m4_bridge_get_expected_weight_bytes(int format, uint32_t K, uint32_t N);
+
+/* m4_mlx_bridge.h:57 -- Y[M,N] (fp16) = X[M,K] (fp16) . W^T, W packed [N, K]. */
+M4_API int m4_bridge_dispatch_gemm(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes, void* Y_ptr,
+                            size_t Y_bytes, int format, uint32_t M, uint32_t K, uint32_t N);
+
+/* m4_mlx_bridge.h:79 -- GEMM with M = 1 (m4_mlx_bridge.mm:293-302). */
+M4_API int m4_bridge_dispatch_gemv(void* x_ptr, size_t x_bytes, void* W_ptr, size_t W_bytes, void* y_ptr,
+                            size_t y_bytes, int format, uint32_t K, uint32_t N);
+
+/* m4_mlx_bridge.h:90 -- waits for all work issued on the bridge stream. */
+M4_API void m4_bridge_synchronize(void);
+
+/* m4_mlx_bridge.h:96 -- process footprint in MB: host resident set plus the
+ * device memory the bridge itself holds. */
+M4_API double m4_bridge_get_uma_footprint_mb(void);
+
+/* m4_mlx_bridge.h:101 */
+M4_API bool m4_bridge_is_initialized(void);
+
+/* m4_mlx_bridge.h:106 -- waits, releases staging memory and the stream. */
+M4_API void m4_bridge_shutdown(void);
+
+/* ---- extensions: same router, other reference routines ------------------ */
+
+/* Validation only: the code m4_bridge_dispatch_gemm would return for these
+ * arguments on an initialized bridge (0 if it would launch), computed without
+ * touching a device (m4_mlx_bridge.mm:204-230). */
+M4_API int m4_bridge_validate_gemm(const void* X_ptr, size_t X_bytes, const void* W_ptr, size_t W_bytes,
+                            const void* Y_ptr, size_t Y_bytes, int format, uint32_t M, uint32_t K,
+                            uint32_t N);
+
+/* Direct-head projection: Y is [H, M, D] with N = H * D; replaces
+ * quant_router_head_gemm_<fmt>_64x64 (quant_router_kernels.metal:754-927,
+ * index map :570-574).  Same validation as dispatch_gemm with N = H * D. */
+M4_API int m4_bridge_dispatch_head_gemm(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes, void* Y_ptr,
+                                 size_t Y_bytes, int format, uint32_t M, uint32_t H, uint32_t D,
+                                 uint32_t K);
+
+/* Projection with a fused residual: Y = fp16(X . W^T + R), R fp16 [M, N];
+ * replaces a GEMM followed by vector_add_residual (unified_kernels.metal:
+ * 78-88; unified_prefill_engine.mm:183-186).  Y may alias R. */
+M4_API int m4_bridge_dispatch_gemm_residual(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes,
+                                     void* R_ptr, size_t R_bytes, void* Y_ptr, size_t Y_bytes,
+                                     int format, uint32_t M, uint32_t K, uint32_t N);
+
+/* Fused dual-projection SwiGLU: Out[M, N_mlp] = silu(X . Wg^T) * (X . Wu^T);
+ * replaces swiglu_mma_dual_simd (brick3_swiglu_kernels.metal:428-698), which
+ * takes Q4_0 only; any projection format 0..3 is accepted here. */
+M4_API int m4_bridge_dispatch_swiglu(void* X_ptr, size_t X_bytes, void* Wg_ptr, size_t Wg_bytes, void* Wu_ptr,
+                              size_t Wu_bytes, void* Out_ptr, size_t Out_bytes, int format, uint32_t M,
+                              uint32_t N_mlp, uint32_t K);
+
+/* Q8_0 quantization of num_blocks groups of 32 fp16 values into 34-byte
+ * blocks; replaces quantize_kv_to_q8_0 (unified_kernels.metal:118-145). */
+M4_API int m4_bridge_quantize_kv_q8_0(void* src_ptr, size_t src_bytes, void* dst_ptr, size_t dst_bytes,
+                               uint64_t num_blocks);
+
+/* Causal flash attention over a Q8_0 KV cache; replaces
+ * flash_attn_mma_64x64_q8_0_d64/_d128 (brick4_attn_kernels.metal:868-911).
+ * Q fp16 [H, M, D]; K_q8, V_q8 Q8_0 blocks over [H, M, D]; D in {64, 128}.
+ * O fp16 [H, M, D] (o_token_major = 0) or [M, H * D] (o_token_major = 1). */
+M4_API int m4_bridge_dispatch_flash_attn_q8_0(void* Q_ptr, size_t Q_bytes, void* Kq_ptr, size_t Kq_bytes,
+                                       void* Vq_ptr, size_t Vq_bytes, void* O_ptr, size_t O_bytes,
+                                       uint32_t H, uint32_t M, uint32_t D, float scale,
+                                       int o_token_major);
+
+/* One prefill layer (no norm, no RoPE), composed as the reference's
+ * TransformerLayerCoordinator::forward (models/transformer_layer.mm:75-218)
+ * with the Q8_0 KV cache of unified_prefill_engine.mm:554-572:
+ *   Q,K,V head GEMMs -> Q8_0(K,V) -> flash attention -> O-proj + residual ->
+ *   fused SwiGLU -> down-proj + residual.
+ * X, X_out fp16 [M, d_model]; Wq/Wk/Wv [H*D, d_model], Wo [d_model, H*D],
+ * Wg/Wu [N_mlp, d_model], Wd [d_model, N_mlp], all in `format`.  Scratch is
+ * held by the bridge.  X_out must not alias X. */
+M4_API int m4_bridge_prefill_layer(void* X_ptr, void* Wq, void* Wk, void* Wv, void* Wo, void* Wg, void* Wu,
+                            void* Wd, void* X_out, int format, uint32_t M, uint32_t d_model, uint32_t H,
+                            uint32_t D, uint32_t N_mlp, float attn_scale);
+
+/* Dequantize W [N, K] to fp16 [N, K] with the kernels' own decoders (the
+ * registry's dequantize hook, src/router/quant_registry.h:24). Formats 0..3. */
+M4_API int m4_bridge_dequantize(void* W_ptr, size_t W_bytes, void* out_ptr, size_t out_bytes, int format,
+                         uint32_t K, uint32_t N);
+
+/* Run subsequent work on `stream` (a hipStream_t, e.g. torch's current
+ * stream); NULL restores the bridge's own stream.  Returns 0 or -1. */
+M4_API int m4_bridge_set_stream(void* stream);
+/* The hipStream_t work is issued on. */
+M4_API void* m4_bridge_get_stream(void);
+/* Text of the last device error seen by the bridge ("" if none). */
+M4_API const char* m4_bridge_last_error(void);
+
+/* ---- format registry (src/router/quant_registry.h:14-65) ---------------- */
+
+typedef struct {
+    int format;
+    const char* name;
+    const char* description;
+    uint32_t block_size;
+    uint64_t struct_size;
+    double bits_per_weight;
+    const char* gemm_kernel_name;
+    const char* head_gemm_kernel_name;
+} m4_quant_codec_info;
+
+/* QuantRegistry::get -- 0 and *out filled, or -3 if unknown. */
+M4_API int m4_registry_get(int format, m4_quant_codec_info* out);
+/* QuantRegistry::get_by_name -- format id or -3. */
+M4_API int m4_registry_get_by_name(const char* name);
+/* QuantRegistry::available_formats -- count; ids written to out[0..cap). */
+M4_API int m4_registry_available_formats(int* out, int cap);
+/* QuantRegistry::compute_weight_bytes -- 0 for an unknown format. */
+M4_API uint64_t m4_registry_compute_weight_bytes(int format, uint64_t num_elements);
+/* QuantRegistry::has_format */
+M4_API bool m4_registry_has_format(int format);
+/* QuantRegistry::register_codec (e.g. QUANT_CUSTOM = 99); strings are copied. */
+M4_API int m4_registry_register_codec(const m4_quant_codec_info* info);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* M4_MLX_BRIDGE_H */

@@ -1,0 +1,457 @@
+// qr_bridge.cpp -- the C-ABI (include/m4_mlx_bridge.h) over the HIP kernels.
+//
+// Mirrors core/bridge/m4_mlx_bridge.mm:79-343: same entry points, same
+// validation order and error codes, asynchronous dispatch + synchronize.
+// Where the reference wraps unified host memory zero-copy (:38-55), this
+// bridge takes device pointers directly and stages anything else (pageable
+// host memory, or device buffers too misaligned for 16-byte vector loads)
+// through bridge-owned device memory.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/m4_mlx_bridge.h"
+#include "qr_formats.h"
+#include "qr_kernels.h"
+
+namespace {
+
+std::mutex g_mu;
+bool g_initialized = false;
+int g_device = 0;
+hipStream_t g_own_stream = nullptr;
+hipStream_t g_stream = nullptr;
+std::string g_last_error;
+
+struct Staged {
+    void* dev;
+    void* host;      // non-null: copy dev -> host at synchronize
+    size_t bytes;
+};
+std::vector<Staged> g_staged;      // freed at synchronize
+size_t g_staged_bytes = 0;
+
+// Grow-only scratch for the layer composition.
+void* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+void set_error(const char* where, hipError_t e) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "%s: %s", where, hipGetErrorString(e));
+    g_last_error = buf;
+}
+
+// Classify a pointer: device-accessible address or null if it must be staged.
+void* device_view(void* p) {
+    hipPointerAttribute_t attr;
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged ||
+        attr.type == hipMemoryTypeUnified)
+        return attr.devicePointer ? attr.devicePointer : p;
+    if (attr.type == hipMemoryTypeHost && attr.devicePointer) return attr.devicePointer;
+    return nullptr;
+}
+
+// Device pointer usable by the kernels for buffer `p`: the pointer itself if it
+// is device memory aligned to `align`, else a staged copy.  For outputs
+// (`out`), the staged copy is written back at synchronize.  Returns null on
+// allocation/copy failure.
+void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
+    void* d = device_view(p);
+    if (d && (reinterpret_cast<uintptr_t>(d) % align) == 0) return d;
+    void* s = nullptr;
+    hipError_t e = hipMalloc(&s, bytes ? bytes : 16);
+    if (e != hipSuccess) {
+        set_error("hipMalloc(staging)", e);
+        return nullptr;
+    }
+    if (in) {
+        e = d ? hipMemcpyAsync(s, d, bytes, hipMemcpyDeviceToDevice, g_stream)
+              : hipMemcpyAsync(s, p, bytes, hipMemcpyHostToDevice, g_stream);
+        if (e != hipSuccess) {
+            set_error("hipMemcpyAsync(stage in)", e);
+            (void)hipFree(s);
+            return nullptr;
+        }
+    }
+    // Device outputs that were only misaligned are copied back on the stream
+    // right after the kernel (see finish_outputs); host outputs at synchronize.
+    g_staged.push_back({s, out ? p : nullptr, bytes});
+    g_staged_bytes += bytes;
+    return s;
+}
+
+// After the launches of one dispatch: device-resident outputs that were staged
+// (misaligned) are copied back in stream order.
+void finish_outputs() {
+    for (auto& st : g_staged) {
+        if (!st.host) continue;
+        void* d = device_view(st.host);
+        if (d) {
+            (void)hipMemcpyAsync(d, st.dev, st.bytes, hipMemcpyDeviceToDevice, g_stream);
+            st.host = nullptr;  // done
+        }
+    }
+}
+
+void sync_and_release() {
+    if (!g_stream) return;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) set_error("hipStreamSynchronize", e);
+    for (auto& st : g_staged) {
+        if (st.host) {
+            e = hipMemcpy(st.host, st.dev, st.bytes, hipMemcpyDeviceToHost);
+            if (e != hipSuccess) set_error("hipMemcpy(stage out)", e);
+        }
+        (void)hipFree(st.dev);
+    }
+    g_staged.clear();
+    g_staged_bytes = 0;
+}
+
+bool is_projection_format(int f) { return f >= 0 && f < 6; }
+bool has_kernels(int f) { return f >= 0 && f < 4; }
+
+// core/bridge/m4_mlx_bridge.mm:204-230, minus the init check.
+int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, size_t Yb, int format,
+             uint32_t M, uint32_t K, uint32_t N) {
+    if (!X || !W || !Y) return -2;
+    if ((reinterpret_cast<uintptr_t>(X) % 2) || (reinterpret_cast<uintptr_t>(Y) % 2)) return -2;
+    if (!is_projection_format(format)) return -3;
+    if (M == 0 || K == 0 || N == 0) return -4;
+    if (K % 32) return -4;
+    if ((format == 2 || format == 4 || format == 5) && (K % 256)) return -4;
+    if (Xb < (size_t)M * K * 2 || Yb < (size_t)M * N * 2 || Wb < qr::expected_weight_bytes(format, K, N))
+        return -2;
+    return 0;
+}
+
+int launch(const qr::GemmParams& p) {
+    hipError_t e = qr::launch_gemm(p, g_stream);
+    if (e != hipSuccess) {
+        set_error("launch_gemm", e);
+        return -6;
+    }
+    return 0;
+}
+
+int gemm_common(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, void* R, int format, uint32_t M,
+                uint32_t K, uint32_t N, uint32_t head_D) {
+    if (!g_initialized) return -1;
+    int rc = validate(X, Xb, W, Wb, Y, Yb, format, M, K, N);
+    if (rc) return rc;
+    if (!has_kernels(format)) return -3;
+    const size_t wbytes = qr::expected_weight_bytes(format, K, N);
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* dx = resolve(X, (size_t)M * K * 2, 16, true, false);
+    void* dw = resolve(W, wbytes, 16, true, false);
+    void* dr = R ? resolve(R, (size_t)M * N * 2, 2, true, false) : nullptr;
+    void* dy = resolve(Y, (size_t)M * N * 2, 2, false, true);
+    if (!dx || !dw || !dy || (R && !dr)) return -5;
+    qr::GemmParams p{};
+    p.format = format;
+    p.X = static_cast<const _Float16*>(dx);
+    p.W = static_cast<const uint8_t*>(dw);
+    p.W2 = nullptr;
+    p.Y = static_cast<_Float16*>(dy);
+    p.R = static_cast<const _Float16*>(dr);
+    p.M = M; p.N = N; p.K = K;
+    p.head_D = head_D;
+    p.col_bytes = wbytes / N;
+    rc = launch(p);
+    finish_outputs();
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+bool m4_bridge_init(const char* /*metallib_path*/) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_initialized) return true;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        g_last_error = "no HIP device";
+        return false;
+    }
+    hipError_t e = hipGetDevice(&g_device);
+    if (e == hipSuccess) e = hipSetDevice(g_device);
+    if (e == hipSuccess) e = hipStreamCreate(&g_own_stream);
+    if (e != hipSuccess) {
+        set_error("init", e);
+        return false;
+    }
+    g_stream = g_own_stream;
+    g_initialized = true;
+    return true;
+}
+
+size_t m4_bridge_get_expected_weight_bytes(int format, uint32_t K, uint32_t N) {
+    return qr::expected_weight_bytes(format, K, N);
+}
+
+int m4_bridge_validate_gemm(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, size_t Yb,
+                            int format, uint32_t M, uint32_t K, uint32_t N) {
+    return validate(X, Xb, W, Wb, Y, Yb, format, M, K, N);
+}
+
+int m4_bridge_dispatch_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format, uint32_t M,
+                            uint32_t K, uint32_t N) {
+    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, N, 0);
+}
+
+int m4_bridge_dispatch_gemv(void* x, size_t xb, void* W, size_t Wb, void* y, size_t yb, int format, uint32_t K,
+                            uint32_t N) {
+    return m4_bridge_dispatch_gemm(x, xb, W, Wb, y, yb, format, 1, K, N);
+}
+
+int m4_bridge_dispatch_head_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format, uint32_t M,
+                                 uint32_t H, uint32_t D, uint32_t K) {
+    if (!g_initialized) return -1;
+    if (H == 0 || D == 0) return -4;
+    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, H * D, D);
+}
+
+int m4_bridge_dispatch_gemm_residual(void* X, size_t Xb, void* W, size_t Wb, void* R, size_t Rb, void* Y, size_t Yb,
+                                     int format, uint32_t M, uint32_t K, uint32_t N) {
+    if (!g_initialized) return -1;
+    if (!R || (reinterpret_cast<uintptr_t>(R) % 2)) return -2;
+    if (Rb < (size_t)M * N * 2) return -2;
+    return gemm_common(X, Xb, W, Wb, Y, Yb, R, format, M, K, N, 0);
+}
+
+int m4_bridge_dispatch_swiglu(void* X, size_t Xb, void* Wg, size_t Wgb, void* Wu, size_t Wub, void* Out,
+                              size_t Outb, int format, uint32_t M, uint32_t Nm, uint32_t K) {
+    if (!g_initialized) return -1;
+    int rc = validate(X, Xb, Wg, Wgb, Out, Outb, format, M, K, Nm);
+    if (rc) return rc;
+    if (!Wu) return -2;
+    if (Wub < qr::expected_weight_bytes(format, K, Nm)) return -2;
+    if (!has_kernels(format)) return -3;
+    const size_t wbytes = qr::expected_weight_bytes(format, K, Nm);
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* dx = resolve(X, (size_t)M * K * 2, 16, true, false);
+    void* dg = resolve(Wg, wbytes, 16, true, false);
+    void* du = resolve(Wu, wbytes, 16, true, false);
+    void* dy = resolve(Out, (size_t)M * Nm * 2, 2, false, true);
+    if (!dx || !dg || !du || !dy) return -5;
+    qr::GemmParams p{};
+    p.format = format;
+    p.X = static_cast<const _Float16*>(dx);
+    p.W = static_cast<const uint8_t*>(dg);
+    p.W2 = static_cast<const uint8_t*>(du);
+    p.Y = static_cast<_Float16*>(dy);
+    p.M = M; p.N = Nm; p.K = K;
+    p.col_bytes = wbytes / Nm;
+    rc = launch(p);
+    finish_outputs();
+    return rc;
+}
+
+int m4_bridge_quantize_kv_q8_0(void* src, size_t src_bytes, void* dst, size_t dst_bytes, uint64_t nblocks) {
+    if (!g_initialized) return -1;
+    if (!src || !dst) return -2;
+    if ((reinterpret_cast<uintptr_t>(src) % 2) || (reinterpret_cast<uintptr_t>(dst) % 2)) return -2;
+    if (nblocks == 0) return -4;
+    if (src_bytes < nblocks * 64 || dst_bytes < nblocks * 34) return -2;
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* ds = resolve(src, nblocks * 64, 16, true, false);
+    void* dd = resolve(dst, nblocks * 34, 2, false, true);
+    if (!ds || !dd) return -5;
+    hipError_t e = qr::launch_quantize_q8_0(static_cast<const _Float16*>(ds), static_cast<uint8_t*>(dd), nblocks,
+                                            g_stream);
+    finish_outputs();
+    if (e != hipSuccess) {
+        set_error("quantize_q8_0", e);
+        return -6;
+    }
+    return 0;
+}
+
+int m4_bridge_dispatch_flash_attn_q8_0(void* Q, size_t Qb, void* Kq, size_t Kqb, void* Vq, size_t Vqb, void* O,
+                                       size_t Ob, uint32_t H, uint32_t M, uint32_t D, float scale,
+                                       int o_token_major) {
+    if (!g_initialized) return -1;
+    if (!Q || !Kq || !Vq || !O) return -2;
+    if ((reinterpret_cast<uintptr_t>(Q) % 2) || (reinterpret_cast<uintptr_t>(O) % 2)) return -2;
+    if (H == 0 || M == 0 || (D != 64 && D != 128)) return -4;
+    const size_t n = (size_t)H * M * D;
+    if (Qb < n * 2 || Ob < n * 2 || Kqb < n / 32 * 34 || Vqb < n / 32 * 34) return -2;
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* dq = resolve(Q, n * 2, 16, true, false);
+    void* dk = resolve(Kq, n / 32 * 34, 4, true, false);
+    void* dv = resolve(Vq, n / 32 * 34, 4, true, false);
+    void* dout = resolve(O, n * 2, 8, false, true);
+    if (!dq || !dk || !dv || !dout) return -5;
+    qr::AttnParams p{static_cast<const _Float16*>(dq), static_cast<const uint8_t*>(dk),
+                     static_cast<const uint8_t*>(dv), static_cast<_Float16*>(dout), H, M, D, scale,
+                     o_token_major ? 1 : 0};
+    hipError_t e = qr::launch_flash_attn_q8_0(p, g_stream);
+    finish_outputs();
+    if (e != hipSuccess) {
+        set_error("flash_attn_q8_0", e);
+        return -6;
+    }
+    return 0;
+}
+
+int m4_bridge_dequantize(void* W, size_t Wb, void* out, size_t outb, int format, uint32_t K, uint32_t N) {
+    if (!g_initialized) return -1;
+    if (!W || !out) return -2;
+    if (!is_projection_format(format)) return -3;
+    if (K == 0 || N == 0 || K % 32) return -4;
+    if (format == 2 && K % 256) return -4;
+    if (!has_kernels(format)) return -3;
+    const size_t wbytes = qr::expected_weight_bytes(format, K, N);
+    if (Wb < wbytes || outb < (size_t)N * K * 2) return -2;
+    if (wbytes >= (1ull << 31)) return -4;
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* dw = resolve(W, wbytes, 16, true, false);
+    void* dout = resolve(out, (size_t)N * K * 2, 16, false, true);
+    if (!dw || !dout) return -5;
+    hipError_t e = qr::launch_dequant(format, static_cast<const uint8_t*>(dw), static_cast<_Float16*>(dout), K, N,
+                                      wbytes / N, g_stream);
+    finish_outputs();
+    if (e != hipSuccess) {
+        set_error("dequant", e);
+        return -6;
+    }
+    return 0;
+}
+
+int m4_bridge_prefill_layer(void* X, void* Wq, void* Wk, void* Wv, void* Wo, void* Wg, void* Wu, void* Wd,
+                            void* Xout, int format, uint32_t M, uint32_t dm, uint32_t H, uint32_t D, uint32_t Nm,
+                            float scale) {
+    if (!g_initialized) return -1;
+    void* ptrs[9] = {X, Wq, Wk, Wv, Wo, Wg, Wu, Wd, Xout};
+    for (void* q : ptrs)
+        if (!q) return -2;
+    if (!has_kernels(format)) return -3;
+    if (M == 0 || dm == 0 || H == 0 || Nm == 0 || (D != 64 && D != 128)) return -4;
+    const uint32_t HD = H * D;
+    const uint32_t bs = qr::get_quant_info(static_cast<qr::QuantFormat>(format)).block_size;
+    if (dm % bs || HD % bs || Nm % bs || dm % 32 || HD % 32 || Nm % 32) return -4;
+    for (void* q : ptrs) {
+        void* d = device_view(q);
+        if (!d || d != q || (reinterpret_cast<uintptr_t>(q) % 16)) return -2;  // device, 16-byte aligned
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t nqkv = (size_t)M * HD;
+    const size_t q8 = nqkv / 32 * 34;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t need = 3 * al(nqkv * 2) + 2 * al(q8) + al(nqkv * 2) + al((size_t)M * dm * 2) + al((size_t)M * Nm * 2);
+    if (need > g_ws_bytes) {
+        if (g_ws) {
+            (void)hipStreamSynchronize(g_stream);
+            (void)hipFree(g_ws);
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+        }
+        hipError_t e = hipMalloc(&g_ws, need);
+        if (e != hipSuccess) {
+            set_error("hipMalloc(layer scratch)", e);
+            return -5;
+        }
+        g_ws_bytes = need;
+    }
+    uint8_t* w = static_cast<uint8_t*>(g_ws);
+    auto take = [&](size_t b) { uint8_t* r = w; w += al(b); return r; };
+    _Float16* q = reinterpret_cast<_Float16*>(take(nqkv * 2));
+    _Float16* k = reinterpret_cast<_Float16*>(take(nqkv * 2));
+    _Float16* v = reinterpret_cast<_Float16*>(take(nqkv * 2));
+    uint8_t* kq = take(q8);
+    uint8_t* vq = take(q8);
+    _Float16* o = reinterpret_cast<_Float16*>(take(nqkv * 2));
+    _Float16* xm = reinterpret_cast<_Float16*>(take((size_t)M * dm * 2));
+    _Float16* s = reinterpret_cast<_Float16*>(take((size_t)M * Nm * 2));
+
+    auto proj = [&](const void* A, const void* W, const void* W2, _Float16* Y, const _Float16* R, uint32_t N,
+                    uint32_t Kd, uint32_t headD) {
+        qr::GemmParams p{};
+        p.format = format;
+        p.X = static_cast<const _Float16*>(A);
+        p.W = static_cast<const uint8_t*>(W);
+        p.W2 = static_cast<const uint8_t*>(W2);
+        p.Y = Y;
+        p.R = R;
+        p.M = M; p.N = N; p.K = Kd;
+        p.head_D = headD;
+        p.col_bytes = qr::expected_weight_bytes(format, Kd, N) / N;
+        return launch(p);
+    };
+    int rc = 0;
+    rc = rc ? rc : proj(X, Wq, nullptr, q, nullptr, HD, dm, D);
+    rc = rc ? rc : proj(X, Wk, nullptr, k, nullptr, HD, dm, D);
+    rc = rc ? rc : proj(X, Wv, nullptr, v, nullptr, HD, dm, D);
+    if (!rc) {
+        hipError_t e = qr::launch_quantize_q8_0(k, kq, nqkv / 32, g_stream);
+        if (e == hipSuccess) e = qr::launch_quantize_q8_0(v, vq, nqkv / 32, g_stream);
+        qr::AttnParams ap{q, kq, vq, o, H, M, D, scale, 1};
+        if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(ap, g_stream);
+        if (e != hipSuccess) {
+            set_error("layer attention", e);
+            rc = -6;
+        }
+    }
+    rc = rc ? rc : proj(o, Wo, nullptr, xm, static_cast<const _Float16*>(X), dm, HD, 0);
+    rc = rc ? rc : proj(xm, Wg, Wu, s, nullptr, Nm, dm, 0);
+    rc = rc ? rc : proj(s, Wd, nullptr, static_cast<_Float16*>(Xout), xm, dm, Nm, 0);
+    return rc;
+}
+
+void m4_bridge_synchronize(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    sync_and_release();
+}
+
+double m4_bridge_get_uma_footprint_mb(void) {
+    long pages = 0, rss = 0;
+    FILE* f = fopen("/proc/self/statm", "r");
+    if (f) {
+        if (fscanf(f, "%ld %ld", &pages, &rss) != 2) rss = 0;
+        fclose(f);
+    }
+    double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
+    return host_mb + (double)(g_ws_bytes + g_staged_bytes) / (1024.0 * 1024.0);
+}
+
+bool m4_bridge_is_initialized(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_initialized;
+}
+
+void m4_bridge_shutdown(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_initialized) return;
+    sync_and_release();
+    if (g_ws) (void)hipFree(g_ws);
+    g_ws = nullptr;
+    g_ws_bytes = 0;
+    if (g_own_stream) (void)hipStreamDestroy(g_own_stream);
+    g_own_stream = nullptr;
+    g_stream = nullptr;
+    g_initialized = false;
+}
+
+int m4_bridge_set_stream(void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_initialized) return -1;
+    g_stream = stream ? static_cast<hipStream_t>(stream) : g_own_stream;
+    return 0;
+}
+
+void* m4_bridge_get_stream(void) { return g_stream; }
+
+const char* m4_bridge_last_error(void) { return g_last_error.c_str(); }
+
+}  // extern "C"

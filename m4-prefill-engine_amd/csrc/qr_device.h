@@ -1,0 +1,73 @@
+// qr_device.h -- gfx950 device helpers shared by the router kernels.
+//
+// Vector types for CDNA4 MFMA operands, buffer-resource loads (bounds-checked
+// in hardware: an offset past num_records reads 0, which the kernels use for
+// ragged M/N edges), and exact fp16 rounding helpers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qr {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+// Third dword of a raw buffer descriptor on gfx9-family parts (32-bit data
+// format, untyped access); num_records is a byte count.
+constexpr int kBufferFlags = 0x00020000;
+// An offset that is always past num_records: loads from it return 0.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
+}
+__device__ __forceinline__ uint32_t ld_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ u2_t ld_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ u4_t ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+__device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ uint32_t f2h_bits(float x) {  // RNE (v_cvt_f16_f32)
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ __forceinline__ uint32_t pack_h2(uint32_t lo16, uint32_t hi16) { return lo16 | (hi16 << 16); }
+
+// Round-to-nearest-even binary16 of the EXACT sum p + q of two floats.
+// The float sum s is made round-to-odd with its TwoSum error term; RNE of a
+// round-to-odd value with >= 2 extra bits equals RNE of the exact value.
+__device__ __forceinline__ uint32_t rne16_sum(float p, float q) {
+    float s = p + q;
+    float bb = s - p;
+    float err = (p - (s - bb)) + (q - bb);
+    uint32_t bits = __builtin_bit_cast(uint32_t, s);
+    if (err != 0.0f && !(bits & 1u)) {
+        bool away = (err > 0.0f) == (s > 0.0f);
+        bits = away ? bits + 1u : bits - 1u;
+    }
+    return f2h_bits(__builtin_bit_cast(float, bits));
+}
+
+// Byte permute: D.byte[i] = sel.byte[i] in 0..3 -> s1.byte, 4..7 -> s0.byte, 0x0c -> 0.
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+// Two 4-bit codes from bytes 0/1 (or 2/3) of a nibble-per-byte word, as the
+// binary16 pair {1024 + c0, 1024 + c1} (magic-exponent conversion: exact).
+__device__ __forceinline__ uint32_t nib_pair_lo(uint32_t x) { return perm(0x64646464u, x, 0x04010400u); }
+__device__ __forceinline__ uint32_t nib_pair_hi(uint32_t x) { return perm(0x64646464u, x, 0x04030402u); }
+
+}  // namespace qr

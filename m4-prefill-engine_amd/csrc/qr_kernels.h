@@ -1,0 +1,39 @@
+// qr_kernels.h -- host-visible launch interface of the router kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qr {
+
+struct GemmParams {
+    int format;
+    const _Float16* X;    // [M, K] fp16, 16-byte aligned
+    const uint8_t* W;     // [N, K] packed blocks, 16-byte aligned
+    const uint8_t* W2;    // second weight matrix (SwiGLU up projection) or null
+    _Float16* Y;          // output
+    const _Float16* R;    // optional residual [M, N] added before rounding, or null
+    uint32_t M, N, K;
+    uint32_t head_D;      // 0: Y is [M, N]; else direct-head [N / head_D, M, head_D]
+    size_t col_bytes;     // bytes of one weight column
+};
+
+hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
+hipError_t launch_dequant(int format, const uint8_t* W, _Float16* out, uint32_t K, uint32_t N, size_t col_bytes,
+                          hipStream_t st);
+
+// Q8_0 quantization of `num_blocks` groups of 32 fp16 values.
+hipError_t launch_quantize_q8_0(const _Float16* src, uint8_t* dst, size_t num_blocks, hipStream_t st);
+
+struct AttnParams {
+    const _Float16* Q;    // [H, M, D]
+    const uint8_t* Kq;    // Q8_0 blocks over [H, M, D]
+    const uint8_t* Vq;    // Q8_0 blocks over [H, M, D]
+    _Float16* O;          // [H, M, D] or token-major [M, H * D]
+    uint32_t H, M, D;
+    float scale;
+    int o_token_major;
+};
+hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st);
+
+}  // namespace qr

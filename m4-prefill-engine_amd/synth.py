@@ -1,0 +1,227 @@
+"""Seeded synthetic inputs for the quantization router.
+
+Two families, both producing the router's packed block layouts (quant_router.h:35-96):
+
+* Random-code generators in the style of the reference benches
+  (bench_universal_router.mm:36-103): random codes and random block scales.
+* Quantizers for the benchmark configurations: fp32 weights drawn from
+  N(0, 0.02) are quantized to Q4_0 (d = absmax/-8), MLX affine groups of 64
+  (scale = (max-min)/15, bias = min; repacked losslessly into the router's
+  32-element MLX blocks), Q4_K (per-sub-block affine fit, 6-bit scales and
+  mins in the reference's packing) and ternary codes with one fp16 scale.
+
+The quantizers only have to be deterministic and self-consistent: parity is
+checked on dequantization and on the projections, not on the quantizer.
+All arrays are numpy; weights are returned as flat uint8 arrays holding
+[N, K / block] blocks in column-major-block order (column n's blocks contiguous).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q4_0, MLX_4BIT, Q4_K, TERNARY_1_58 = 0, 1, 2, 3
+BLOCK_ELEMS = {0: 32, 1: 32, 2: 256, 3: 32, 4: 256, 5: 256, 6: 32, 7: 128}
+BLOCK_BYTES = {0: 18, 1: 20, 2: 144, 3: 12, 4: 160, 5: 144, 6: 34, 7: 34}
+
+
+def _h16_bytes(x: np.ndarray) -> np.ndarray:
+    """fp32 array [...] -> uint8 [..., 2] little-endian binary16 (RNE)."""
+    return np.ascontiguousarray(x.astype(np.float16)).view(np.uint8).reshape(*x.shape, 2)
+
+
+def activations(M: int, K: int, seed: int, std: float = 1.0) -> np.ndarray:
+    """X ~ N(0, std^2) as fp16 [M, K]."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((M, K), dtype=np.float32) * np.float32(std)).astype(np.float16)
+
+
+def gaussian_weights(N: int, K: int, seed: int, std: float = 0.02) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((N, K), dtype=np.float32) * np.float32(std)
+
+
+def _pack_nibbles32(q: np.ndarray) -> np.ndarray:
+    """q [..., 32] codes 0..15 -> [..., 16] bytes: byte i = q[i] | q[i+16] << 4."""
+    q = q.astype(np.uint8)
+    return (q[..., :16] | (q[..., 16:] << 4)).astype(np.uint8)
+
+
+# ---------------------------------------------------------------------------
+# Quantizers for the benchmark configurations
+# ---------------------------------------------------------------------------
+
+def quantize_q4_0(w: np.ndarray) -> np.ndarray:
+    """[N, K] fp32 -> Q4_0 blocks: d = m / -8 with m the signed absmax value,
+    q = clamp(floor(w / d + 8.5), 0, 15)."""
+    N, K = w.shape
+    assert K % 32 == 0
+    b = w.reshape(N, K // 32, 32).astype(np.float32)
+    idx = np.abs(b).argmax(axis=-1)
+    m = np.take_along_axis(b, idx[..., None], axis=-1)[..., 0]
+    d = m / np.float32(-8.0)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), 0).astype(np.float32)
+    q = np.clip(np.floor(b * inv[..., None] + np.float32(8.5)), 0, 15).astype(np.uint8)
+    out = np.empty((N, K // 32, 18), np.uint8)
+    out[..., 0:2] = _h16_bytes(d)
+    out[..., 2:] = _pack_nibbles32(q)
+    return out.reshape(-1)
+
+
+def quantize_mlx_g64(w: np.ndarray):
+    """[N, K] fp32 -> MLX-style affine groups of 64: (scales fp16 [N, K/64],
+    biases fp16 [N, K/64], packed uint32 [N, K/8] with 8 codes per word, LSB first)."""
+    N, K = w.shape
+    assert K % 64 == 0
+    g = w.reshape(N, K // 64, 64).astype(np.float32)
+    mn, mx = g.min(-1), g.max(-1)
+    scale = ((mx - mn) / np.float32(15.0)).astype(np.float16)
+    bias = mn.astype(np.float16)
+    s32, b32 = scale.astype(np.float32), bias.astype(np.float32)
+    safe = np.where(s32 != 0, s32, 1)
+    q = np.where(s32[..., None] != 0, np.rint((g - b32[..., None]) / safe[..., None]), 0)
+    q = np.clip(q, 0, 15).astype(np.uint32).reshape(N, K // 8, 8)
+    packed = np.zeros((N, K // 8), np.uint32)
+    for j in range(8):
+        packed |= q[..., j] << np.uint32(4 * j)
+    return scale, bias, packed
+
+
+def mlx_g64_to_router_blocks(scale: np.ndarray, bias: np.ndarray, packed: np.ndarray) -> np.ndarray:
+    """Lossless repack of MLX g64 groups into the router's 32-element MLX_4BIT
+    blocks (quant_router.h:41-45): each group becomes two blocks with the same
+    d and bias; codes are re-packed byte i = q[i] | q[i+16] << 4."""
+    N, G = scale.shape
+    K = G * 64
+    codes = np.zeros((N, K // 8, 8), np.uint8)
+    for j in range(8):
+        codes[..., j] = (packed >> np.uint32(4 * j)) & np.uint32(0xF)
+    codes = codes.reshape(N, K // 32, 32)
+    out = np.empty((N, K // 32, 20), np.uint8)
+    out[..., 0:2] = np.repeat(scale.view(np.uint8).reshape(N, G, 2), 2, axis=1)
+    out[..., 2:4] = np.repeat(bias.view(np.uint8).reshape(N, G, 2), 2, axis=1)
+    out[..., 4:] = _pack_nibbles32(codes)
+    return out.reshape(-1)
+
+
+def quantize_mlx_4bit(w: np.ndarray) -> np.ndarray:
+    return mlx_g64_to_router_blocks(*quantize_mlx_g64(w))
+
+
+def _pack_q4k_scales(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """sc, mn [..., 8] 6-bit -> scales[12] in the reference's packing
+    (bench_universal_router.mm:70-78; decoded at cpu_gold_reference.h:121-127)."""
+    sc = sc.astype(np.uint8)
+    mn = mn.astype(np.uint8)
+    s = np.empty((*sc.shape[:-1], 12), np.uint8)
+    s[..., 0:4] = (sc[..., 0:4] & 63) | ((mn[..., 0:4] >> 4) << 6)
+    s[..., 4:8] = (sc[..., 4:8] & 63) | ((mn[..., 4:8] >> 4) << 6)
+    s[..., 8:12] = (mn[..., 0:4] & 15) | ((mn[..., 4:8] & 15) << 4)
+    return s
+
+
+def quantize_q4_k(w: np.ndarray) -> np.ndarray:
+    """[N, K] fp32 -> Q4_K super-blocks: per 32-element sub-block an affine fit
+    (scale = (max-min)/15, min = -min(w) clipped at 0), 6-bit sc/m against the
+    super-block d = max(scale)/63 and dmin = max(min)/63."""
+    N, K = w.shape
+    assert K % 256 == 0
+    b = w.reshape(N, K // 256, 8, 32).astype(np.float32)
+    lo = np.minimum(b.min(-1), 0)
+    hi = b.max(-1)
+    scale = (hi - lo) / np.float32(15.0)
+    minv = -lo
+    d = (scale.max(-1) / np.float32(63.0)).astype(np.float16)
+    dmin = (minv.max(-1) / np.float32(63.0)).astype(np.float16)
+    d32, dm32 = d.astype(np.float32), dmin.astype(np.float32)
+    sc = np.clip(np.rint(scale / np.where(d32 != 0, d32, 1)[..., None]), 0, 63)
+    sc = np.where(d32[..., None] != 0, sc, 0).astype(np.uint8)
+    mm = np.clip(np.rint(minv / np.where(dm32 != 0, dm32, 1)[..., None]), 0, 63)
+    mm = np.where(dm32[..., None] != 0, mm, 0).astype(np.uint8)
+    A = d32[..., None] * sc.astype(np.float32)
+    B = dm32[..., None] * mm.astype(np.float32)
+    q = np.where(A[..., None] != 0, np.rint((b + B[..., None]) / np.where(A != 0, A, 1)[..., None]), 0)
+    q = np.clip(q, 0, 15).astype(np.uint8)
+    out = np.empty((N, K // 256, 144), np.uint8)
+    out[..., 0:2] = _h16_bytes(d.astype(np.float32))
+    out[..., 2:4] = _h16_bytes(dmin.astype(np.float32))
+    out[..., 4:16] = _pack_q4k_scales(sc, mm)
+    out[..., 16:] = _pack_nibbles32(q).reshape(N, K // 256, 128)
+    return out.reshape(-1)
+
+
+def _pack_ternary(codes: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """codes [N, nb, 32] in 0..3, d [N, nb] fp32 -> 12-byte blocks
+    {d, pad, u32 qs[2]}, element j at bits 2j of qs[j // 16]."""
+    N, nb, _ = codes.shape
+    c = codes.astype(np.uint32).reshape(N, nb, 2, 16)
+    words = np.zeros((N, nb, 2), np.uint32)
+    for j in range(16):
+        words |= c[..., j] << np.uint32(2 * j)
+    out = np.zeros((N, nb, 12), np.uint8)
+    out[..., 0:2] = _h16_bytes(d)
+    out[..., 4:12] = words.view(np.uint8).reshape(N, nb, 8)
+    return out.reshape(-1)
+
+
+def ternary_weights(N: int, K: int, seed: int, scale: float = 0.02) -> np.ndarray:
+    """BitNet-style weights {-1, 0, +1} with p = {.25, .5, .25} and ONE fp16
+    per-tensor scale, replicated into every 32-element block's d."""
+    rng = np.random.default_rng(seed)
+    u = rng.random((N, K // 32, 32))
+    codes = np.where(u < 0.25, 0, np.where(u < 0.75, 1, 2)).astype(np.uint8)
+    d = np.full((N, K // 32), np.float32(scale))
+    return _pack_ternary(codes, d)
+
+
+def quantized_weights(fmt: int, N: int, K: int, seed: int, std: float = 0.02) -> np.ndarray:
+    """Benchmark-configuration weights for `fmt` (N(0, std) before quantization)."""
+    if fmt == TERNARY_1_58:
+        return ternary_weights(N, K, seed)
+    w = gaussian_weights(N, K, seed, std)
+    if fmt == Q4_0:
+        return quantize_q4_0(w)
+    if fmt == MLX_4BIT:
+        return quantize_mlx_4bit(w)
+    if fmt == Q4_K:
+        return quantize_q4_k(w)
+    raise ValueError(f"no quantizer for format {fmt}")
+
+
+# ---------------------------------------------------------------------------
+# Random-code generators (reference bench style)
+# ---------------------------------------------------------------------------
+
+def random_blocks(fmt: int, N: int, K: int, seed: int, code3: bool = False) -> np.ndarray:
+    """Random codes and random scales in the ranges the reference benches draw
+    them from (bench_universal_router.mm:36-103).  For ternary, code 3 is
+    emitted only if `code3` (the reference's generators never emit it)."""
+    rng = np.random.default_rng(seed)
+    nb = K // BLOCK_ELEMS[fmt]
+    if fmt == Q4_0:
+        out = np.empty((N, nb, 18), np.uint8)
+        out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.04 + 0.002).astype(np.float32))
+        out[..., 2:] = rng.integers(0, 256, (N, nb, 16), dtype=np.uint8)
+    elif fmt == MLX_4BIT:
+        out = np.empty((N, nb, 20), np.uint8)
+        out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.03 + 0.001).astype(np.float32))
+        out[..., 2:4] = _h16_bytes((rng.random((N, nb)) * 0.1 - 0.05).astype(np.float32))
+        out[..., 4:] = rng.integers(0, 256, (N, nb, 16), dtype=np.uint8)
+    elif fmt == Q4_K:
+        out = np.empty((N, nb, 144), np.uint8)
+        out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.002 + 0.0002).astype(np.float32))
+        out[..., 2:4] = _h16_bytes((rng.random((N, nb)) * 0.001 + 0.0001).astype(np.float32))
+        sc = rng.integers(1, 64, (N, nb, 8))
+        mn = rng.integers(0, 63, (N, nb, 8))
+        out[..., 4:16] = _pack_q4k_scales(sc, mn)
+        out[..., 16:] = rng.integers(0, 256, (N, nb, 128), dtype=np.uint8)
+    elif fmt == TERNARY_1_58:
+        codes = rng.integers(0, 4 if code3 else 3, (N, nb, 32), dtype=np.uint8)
+        d = (rng.random((N, nb)) * 0.05 + 0.01).astype(np.float32)
+        return _pack_ternary(codes, d)
+    else:
+        raise ValueError(f"no random generator for format {fmt}")
+    return out.reshape(-1)
+
+
+def weight_bytes(fmt: int, K: int, N: int) -> int:
+    return (K // BLOCK_ELEMS[fmt]) * N * BLOCK_BYTES[fmt]

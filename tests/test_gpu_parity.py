@@ -1,0 +1,299 @@
+"""GPU parity: the HIP kernels, called through the C-ABI, against the oracle.
+
+Bars: dequantized weights and Q8_0 codes bit-exact;
+projections, SwiGLU and attention within max |diff| <= 1/128 = 0.0078125 of
+the double-precision CPU gold (tests/e2e/test_tier1_feature_coverage.mm:149;
+core/metrology/bench_standards.h:28).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import synth
+import tolerance
+from tolerance import TOL
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def empty16(*shape):
+    import torch
+
+    return torch.empty(*shape, dtype=torch.float16, device="cuda")
+
+
+def maxdiff(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    assert np.all(np.isfinite(a)), "non-finite GPU output"
+    return float(np.max(np.abs(a - b))) if a.size else 0.0
+
+
+def absxw(oracle, fmt, X, W, K, N):
+    """sum_k |x_k w_k| with the exact weights (error-bound scale)."""
+    return np.abs(X.astype(np.float64)) @ np.abs(oracle.dequantize_f64(fmt, W, K, N)).T
+
+
+def weights(kind, fmt, N, K, seed):
+    return synth.random_blocks(fmt, N, K, seed) if kind == "random" else synth.quantized_weights(fmt, N, K, seed)
+
+
+# --------------------------------------------------------------------------
+# Dequantization: bit-exact
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt,K", [(0, 512), (0, 96), (1, 512), (1, 96), (2, 512), (3, 512), (3, 96)])
+@pytest.mark.parametrize("kind", ["random", "quantized"])
+def test_dequant_bit_exact(bridge, oracle, fmt, K, kind):
+    N = 72
+    if kind == "quantized" and fmt == 1 and K % 64:
+        pytest.skip("MLX g64 quantizer needs K % 64 == 0")
+    W = weights(kind, fmt, N, K, 100 + fmt)
+    out = empty16(N, K)
+    bridge.dequantize(dev(W), out, fmt, K, N)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(out).view(np.uint16), oracle.dequantize(fmt, W, K, N).view(np.uint16))
+
+
+def test_dequant_ternary_code3_and_q4k_slow_path(bridge, oracle):
+    W = synth.random_blocks(3, 40, 256, 7, code3=True)
+    out = empty16(40, 256)
+    bridge.dequantize(dev(W), out, 3, 256, 40)
+    # Q4_K with d >> dmin (binade gap > 3): exact-sum path
+    Wk = synth.random_blocks(2, 40, 512, 8).reshape(40, 2, 144).copy()
+    rng = np.random.default_rng(9)
+    Wk[..., 0:2] = np.float16(3.0).reshape(1).view(np.uint8)
+    Wk[..., 2:4] = (rng.random((40, 2)) * 1e-4).astype(np.float16)[..., None].view(np.uint8)
+    Wk = Wk.reshape(-1)
+    outk = empty16(40, 512)
+    bridge.dequantize(dev(Wk), outk, 2, 512, 40)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(out).view(np.uint16), oracle.dequantize(3, W, 256, 40).view(np.uint16))
+    np.testing.assert_array_equal(host(outk).view(np.uint16), oracle.dequantize(2, Wk, 512, 40).view(np.uint16))
+
+
+# --------------------------------------------------------------------------
+# Projections
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [1, 33, 127, 128, 129, 2048])
+def test_gemm_tier1_shapes(bridge, oracle, fmt, M):
+    # tests/e2e/test_tier1_feature_coverage.mm:122-223: K=512, N=256
+    K, N = 512, 256
+    X = synth.activations(M, K, M, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 7 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    ref = oracle.gemm(fmt, X, W, N)
+    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, fmt, X, W, K, N), K))
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("M,K,N", [(64, 256, 96), (200, 1024, 160), (31, 2304, 64)])
+def test_gemm_gaussian_quantized(bridge, oracle, fmt, M, K, N):
+    if fmt == 1 and K % 64:
+        pytest.skip("g64")
+    X = synth.activations(M, K, 3)
+    W = synth.quantized_weights(fmt, N, K, 4)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    assert maxdiff(host(Y), oracle.gemm(fmt, X, W, N)) <= TOL
+
+
+@pytest.mark.parametrize("N", [33, 65])
+def test_gemm_ragged_n_known_answer(bridge, N):
+    # tests/redteam_bridge.py:438-455: N not divisible by the tile, X = 1, w = 1 -> K
+    M, K = 32, 64
+    blk = np.concatenate([np.array([0x00, 0x3C], np.uint8), np.full(16, 0x99, np.uint8)])
+    W = np.tile(blk, (K // 32) * N)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(np.ones((M, K), np.float16)), dev(W), Y, 0, M, K, N)
+    bridge.synchronize()
+    assert np.all(host(Y) == K)
+
+
+def test_bridge_basic_known_answers_host_buffers(bridge):
+    """tests/test_bridge_basic.py:41-150 with host (numpy) buffers: the bridge
+    stages them through device memory and writes Y back at synchronize()."""
+    for M, K, N in [(33, 64, 64), (64, 64, 64), (128, 128, 128)]:
+        blk = np.concatenate([np.array([0x00, 0x3C], np.uint8), np.full(16, 0x99, np.uint8)])
+        W = np.tile(blk, (K // 32) * N)
+        Y = np.zeros((M, N), np.float16)
+        bridge.dispatch_gemm(np.ones((M, K), np.float16), W, Y, 0, M, K, N, check_finite=True)
+        bridge.synchronize()
+        assert np.all(Y == K)
+    M = K = N = 64
+    blk = np.concatenate([np.array([0x00, 0x3C, 0x00, 0x00], np.uint8), np.full(16, 0x11, np.uint8)])
+    Y = np.zeros((M, N), np.float16)
+    bridge.dispatch_gemm(np.ones((M, K), np.float16), np.tile(blk, (K // 32) * N), Y, 1, M, K, N)
+    bridge.synchronize()
+    assert np.all(Y == K)
+    # decode GEMV (test_bridge_basic.py:121-150)
+    blk = np.concatenate([np.array([0x00, 0x3C], np.uint8), np.full(16, 0x99, np.uint8)])
+    y = np.zeros(N, np.float16)
+    bridge.dispatch_gemv(np.ones(K, np.float16), np.tile(blk, (K // 32) * N), y, 0)
+    bridge.synchronize()
+    assert np.all(y == K)
+
+
+def test_gemv_and_misaligned_pointers(bridge, oracle):
+    import torch
+
+    K, N = 512, 128
+    W = synth.random_blocks(2, N, K, 11)
+    x = synth.activations(1, K, 12)
+    y = empty16(N)
+    bridge.dispatch_gemv(dev(x[0]), dev(W), y, 2)
+    # X, W and Y at 2-byte offsets: accepted (only odd pointers are refused), staged internally
+    xb = torch.zeros(K + 1, dtype=torch.float16, device="cuda")
+    xb[1:] = dev(x[0])
+    wb = torch.zeros(W.size + 2, dtype=torch.uint8, device="cuda")
+    wb[2:] = dev(W)
+    yb = torch.zeros(N + 1, dtype=torch.float16, device="cuda")
+    lib = bridge.lib
+    rc = lib.m4_bridge_dispatch_gemv(xb.data_ptr() + 2, K * 2, wb.data_ptr() + 2, W.size, yb.data_ptr() + 2,
+                                     N * 2, 2, K, N)
+    assert rc == 0
+    assert lib.m4_bridge_dispatch_gemv(xb.data_ptr() + 1, K * 2, wb.data_ptr(), W.size, yb.data_ptr(), N * 2, 2,
+                                       K, N) == -2
+    bridge.synchronize()
+    ref = oracle.gemm(2, x, W, N)[0]
+    tolerance.check(host(y), ref, tolerance.gemm_bound(ref, absxw(oracle, 2, x, W, K, N)[0], K))
+    np.testing.assert_array_equal(host(yb)[1:], host(y))
+
+
+@pytest.mark.parametrize("fmt", [0, 2, 3])
+def test_direct_head_and_residual(bridge, oracle, fmt):
+    M, K, H, D = 129, 512, 4, 64
+    N = H * D
+    X = synth.activations(M, K, 21)
+    W = synth.random_blocks(fmt, N, K, 22)
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    R = synth.activations(M, N, 23)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    bridge.synchronize()
+    axw = absxw(oracle, fmt, X, W, K, N)
+    ref = oracle.gemm(fmt, X, W, N)
+    refh = oracle.gemm(fmt, X, W, N, head_D=D)
+    tolerance.check(host(Yh), refh, tolerance.gemm_bound(ref, axw, K).reshape(M, H, D).transpose(1, 0, 2))
+    refr = oracle.gemm(fmt, X, W, N, R=R)
+    tolerance.check(host(Yr), refr, tolerance.gemm_bound(refr, axw, K))
+
+
+# --------------------------------------------------------------------------
+# SwiGLU
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [33, 128, 129])
+def test_swiglu(bridge, oracle, fmt, M):
+    # brick3_swiglu_bench.mm:268-426 verifies M in {33,127,128,129}
+    K, N = 512, 256
+    X = synth.activations(M, K, 31, std=0.35)
+    Wg, Wu = synth.random_blocks(fmt, N, K, 32), synth.random_blocks(fmt, N, K, 33)
+    out = empty16(M, N)
+    bridge.dispatch_swiglu(dev(X), dev(Wg), dev(Wu), out, fmt, M, N, K)
+    bridge.synchronize()
+    ref = oracle.swiglu(fmt, X, Wg, Wu, N)
+    Xd = X.astype(np.float64)
+    Wgd, Wud = oracle.dequantize_f64(fmt, Wg, K, N), oracle.dequantize_f64(fmt, Wu, K, N)
+    g, u = Xd @ Wgd.T, Xd @ Wud.T
+    bound = tolerance.swiglu_bound(ref, g, u, np.abs(Xd) @ np.abs(Wgd).T, np.abs(Xd) @ np.abs(Wud).T, K)
+    tolerance.check(host(out), ref, bound)
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+def test_swiglu_gaussian_strict(bridge, oracle, fmt):
+    """BASELINE-distribution inputs: flat 1/128."""
+    M, K, N = 160, 1024, 192
+    X = synth.activations(M, K, 34)
+    Wg, Wu = synth.quantized_weights(fmt, N, K, 35), synth.quantized_weights(fmt, N, K, 36)
+    out = empty16(M, N)
+    bridge.dispatch_swiglu(dev(X), dev(Wg), dev(Wu), out, fmt, M, N, K)
+    bridge.synchronize()
+    assert maxdiff(host(out), oracle.swiglu(fmt, X, Wg, Wu, N)) <= TOL
+
+
+# --------------------------------------------------------------------------
+# Q8_0 KV cache and attention
+# --------------------------------------------------------------------------
+
+def test_quantize_kv_q8_0_bit_exact(bridge, oracle):
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((4096, 32)) * 10.0 ** rng.integers(-5, 4, (4096, 1))).astype(np.float16)
+    x[0] = 0
+    x[1, 5] = np.float16(-65504)
+    q = __import__("torch").empty(x.shape[0] * 34, dtype=__import__("torch").uint8, device="cuda")
+    bridge.quantize_kv_q8_0(dev(x), q)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(q), oracle.quantize_q8_0(x))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("M", [1, 33, 127, 128, 129, 256])
+def test_flash_attention_q8_0(bridge, oracle, D, M):
+    # brick4_attn_bench.mm:216-327: H=8, M in {33,127,128,129,256}, D in {64,128}
+    import torch
+
+    H = 8
+    rng = np.random.default_rng(M * D)
+    Q, K, V = ((rng.standard_normal((H, M, D)) * 0.35).astype(np.float16) for _ in range(3))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    O = empty16(H, M, D)
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), O, H, M, D, scale)
+    Ot = empty16(M, H * D)
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), Ot, H, M, D, scale, o_token_major=True)
+    bridge.synchronize()
+    ref = oracle.attention_q8_0(Q, Kq, Vq, scale)
+    assert maxdiff(host(O), ref) <= TOL
+    np.testing.assert_array_equal(host(Ot).reshape(M, H, D).transpose(1, 0, 2), host(O))
+    assert torch.isfinite(O).all()
+
+
+def test_flash_attention_unit_scale_inputs(bridge, oracle):
+    """N(0,1) activations (BASELINE config 5 scale): larger logits."""
+    H, M, D = 4, 300, 64
+    rng = np.random.default_rng(5)
+    Q, K, V = (rng.standard_normal((H, M, D)).astype(np.float16) for _ in range(3))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    O = empty16(H, M, D)
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), O, H, M, D, 0.125)
+    bridge.synchronize()
+    assert maxdiff(host(O), oracle.attention_q8_0(Q, Kq, Vq, 0.125)) <= TOL
+
+
+# --------------------------------------------------------------------------
+# Layer
+# --------------------------------------------------------------------------
+
+def test_prefill_layer_small(bridge, oracle):
+    M, dm, H, D, Nm = 192, 256, 4, 64, 512
+    X = synth.activations(M, dm, 51)
+    shapes = [(H * D, dm)] * 3 + [(dm, H * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    Ws = [synth.quantized_weights(0, n, k, 60 + i) for i, (n, k) in enumerate(shapes)]
+    out = empty16(M, dm)
+    bridge.prefill_layer(dev(X), *[dev(w) for w in Ws], out, 0, M, dm, H, D, Nm, 0.125)
+    bridge.synchronize()
+    ref = oracle.layer(0, X, *Ws, H=H, D=D, N_mlp=Nm, scale=0.125)
+    d = maxdiff(host(out), ref)
+    print(f"layer max|diff| = {d}")
+    # Intermediates are fp16 on both sides; an fp16 tie flipped upstream can move
+    # a downstream value by about one output ulp (|y| < 8 -> ulp <= 2^-8).
+    assert d <= 2 * TOL

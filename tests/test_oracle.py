@@ -1,0 +1,325 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each check is chosen so a plausible mistake in the restatement fails it:
+known-answer tests from the reference's own suites, layout probes (one code
+set at a time), closed forms at exactly representable scales, agreement of
+the reference's two independent texts (its generator's packing vs its gold's
+unpacking), an independent IEEE implementation (numpy) for the fp16
+rounding, and brute-force numpy evaluation of the reductions.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import synth
+
+F16_ONE = np.array([1.0], np.float16).view(np.uint8)
+
+
+def _f16(x):
+    return np.array([x], np.float16).view(np.uint8)
+
+
+# --------------------------------------------------------------------------
+# binary16 conversions
+# --------------------------------------------------------------------------
+
+def test_f16_roundtrip_exhaustive(oracle):
+    h = np.arange(65536, dtype=np.uint16).view(np.float16)
+    finite = np.isfinite(h)
+    d = oracle.f16_to_f64(h)
+    np.testing.assert_array_equal(d[finite], h[finite].astype(np.float64))
+    back = oracle.f64_to_f16(d[finite])
+    np.testing.assert_array_equal(back.view(np.uint16), h[finite].view(np.uint16))
+
+
+def test_f64_to_f16_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200000) * 10.0 ** rng.integers(-9, 5, 200000),
+        # exact ties between adjacent halves, both parities, incl. subnormals
+        (np.arange(-3000, 3000) + 0.5) * 2.0 ** -24,
+        (np.arange(1024, 2048) + 0.5) * 2.0 ** -10,
+        np.array([65504.0, 65519.99, 65520.0, -65520.0, 1e-9, -1e-9, 0.0, -0.0]),
+    ])
+    ours = oracle.f64_to_f16(x).view(np.uint16)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)  # numpy: single RNE rounding
+    np.testing.assert_array_equal(ours, ref)
+
+
+# --------------------------------------------------------------------------
+# Dequantization: known answers and layout probes
+# --------------------------------------------------------------------------
+
+def _q4_0_block(d, qs):
+    return np.concatenate([_f16(d), np.asarray(qs, np.uint8)])
+
+
+def test_q4_0_kat_nibble8_is_zero(oracle):
+    # tests/e2e/test_tier1_feature_coverage.mm:248-257
+    w = oracle.dequantize(0, _q4_0_block(0.5, [0x88] * 16), 32, 1)
+    assert np.all(w == 0)
+
+
+def test_q4_0_layout_and_values(oracle):
+    # byte i low nibble -> element i, high nibble -> element i+16; w = (q-8)*d
+    for i in range(16):
+        for hi in (False, True):
+            for q in range(16):
+                qs = np.full(16, 0x88, np.uint8)
+                qs[i] = (q << 4 | 8) if hi else (0x80 | q)
+                w = oracle.dequantize(0, _q4_0_block(0.25, qs), 32, 1)[0].astype(np.float64)
+                exp = np.zeros(32)
+                exp[i + 16 if hi else i] = (q - 8) * 0.25
+                np.testing.assert_array_equal(w, exp)
+
+
+def test_mlx_kat(oracle):
+    # d = 0, bias = 0.5: every weight 0.5 (test_tier1_feature_coverage.mm:287-297)
+    blk = np.concatenate([_f16(0.0), _f16(0.5), np.full(16, 0x37, np.uint8)])
+    w = oracle.dequantize(1, blk, 32, 1)
+    assert np.all(w == 0.5) and float(w.astype(np.float64).sum()) == 16.0
+    # w = q*d + bias: probe every code at an exact scale
+    for q in range(16):
+        blk = np.concatenate([_f16(0.125), _f16(-1.0), np.full(16, q | (q << 4), np.uint8)])
+        assert np.all(oracle.dequantize(1, blk, 32, 1) == q * 0.125 - 1.0)
+
+
+def test_ternary_kat_and_layout(oracle):
+    # 0x55555555 = code 1 everywhere -> 0 (test_tier1_feature_coverage.mm:363-376)
+    blk = np.concatenate([_f16(0.75), np.zeros(2, np.uint8),
+                          np.array([0x55555555, 0x55555555], np.uint32).view(np.uint8)])
+    assert np.all(oracle.dequantize(3, blk, 32, 1) == 0)
+    # element j <- bits 2j of qs[j // 16]; code c -> (c-1)*d, code 3 -> +2d (CPU gold)
+    for j in range(32):
+        for c in range(4):
+            words = np.array([0x55555555, 0x55555555], np.uint32)
+            words[j // 16] = (words[j // 16] & ~np.uint32(3 << (2 * (j % 16)))) | np.uint32(c << (2 * (j % 16)))
+            blk = np.concatenate([_f16(0.5), np.zeros(2, np.uint8), words.view(np.uint8)])
+            w = oracle.dequantize(3, blk, 32, 1)[0].astype(np.float64)
+            exp = np.zeros(32)
+            exp[j] = (c - 1) * 0.5
+            np.testing.assert_array_equal(w, exp)
+
+
+def test_q4_k_scale_packing_agrees_with_reference_generator(oracle):
+    """The reference packs (sc, min) in its generator (bench_universal_router.mm:
+    70-78) and unpacks them in its gold (cpu_gold_reference.h:121-127); synth
+    restates the former, the oracle the latter.  With d = dmin = 1, q = 0 gives
+    -min and q = 1 gives sc - min for every sub-block."""
+    rng = np.random.default_rng(1)
+    for trial in range(64):
+        sc = rng.integers(0, 64, 8) if trial else np.arange(8) * 9
+        mn = rng.integers(0, 64, 8) if trial else 63 - np.arange(8) * 9
+        blk = np.zeros(144, np.uint8)
+        blk[0:2] = _f16(1.0)
+        blk[2:4] = _f16(1.0)
+        blk[4:16] = synth._pack_q4k_scales(sc[None], mn[None])[0]
+        blk[16:] = 0x10  # low nibble 0 (elements 0..15), high nibble 1 (16..31) of each sub-block
+        w = oracle.dequantize(2, blk, 256, 1)[0].astype(np.float64).reshape(8, 32)
+        np.testing.assert_array_equal(w[:, :16], np.repeat(-mn[:, None].astype(float), 16, 1))
+        np.testing.assert_array_equal(w[:, 16:], np.repeat((sc - mn)[:, None].astype(float), 16, 1))
+
+
+def test_q4_k_sub_block_qs_layout(oracle):
+    # sub-block s uses qs[16s .. 16s+15]; byte i -> elements 32s+i and 32s+i+16
+    for s in range(8):
+        for i in (0, 7, 15):
+            blk = np.zeros(144, np.uint8)
+            blk[0:2] = _f16(0.5)
+            blk[4:16] = synth._pack_q4k_scales(np.full((1, 8), 2), np.zeros((1, 8), int))[0]
+            blk[16 + 16 * s + i] = 0x31
+            w = oracle.dequantize(2, blk, 256, 1)[0].astype(np.float64)
+            exp = np.zeros(256)
+            exp[32 * s + i] = 1 * 0.5 * 2
+            exp[32 * s + i + 16] = 3 * 0.5 * 2
+            np.testing.assert_array_equal(w, exp)
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+def test_dequant_f64_rounds_to_dequant(oracle, fmt):
+    W = synth.random_blocks(fmt, 8, 512, 40 + fmt)
+    np.testing.assert_array_equal(oracle.dequantize_f64(fmt, W, 512, 8).astype(np.float16),
+                                  oracle.dequantize(fmt, W, 512, 8))
+
+
+def test_dequant_single_rounding_q4_k(oracle):
+    """q*(d*sc) - dmin*m is rounded ONCE to fp16 (no fp16 intermediate)."""
+    rng = np.random.default_rng(2)
+    W = synth.random_blocks(2, 16, 512, 3)
+    w = oracle.dequantize(2, W, 512, 16).astype(np.float64)
+    blk = W.reshape(16, 2, 144)
+    d = blk[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    dmin = blk[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    # decode sc/min through the generator-side packing inverse (independent: bit masks per the header)
+    s = blk[..., 4:16].astype(np.int64)
+    sc = np.concatenate([s[..., 0:4] & 63, s[..., 4:8] & 63], -1)
+    mn = np.concatenate([(s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4),
+                         (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)], -1)
+    qs = blk[..., 16:].reshape(16, 2, 8, 16).astype(np.int64)
+    q = np.concatenate([qs & 15, qs >> 4], -1)  # [n, sb, s, 32]
+    exact = q * (d[..., None, None] * sc[..., None]) - (dmin[..., None, None] * mn[..., None])
+    np.testing.assert_array_equal(w.reshape(exact.shape), exact.astype(np.float16).astype(np.float64))
+    assert rng is not None
+
+
+# --------------------------------------------------------------------------
+# Projections
+# --------------------------------------------------------------------------
+
+def test_bridge_kat_q4_0_ones(oracle):
+    # tests/test_bridge_basic.py:41-83: d = 1.0 (0x3C00), nibbles 0x99 -> w = 1; X = 1 -> Y = K
+    for M, K, N in [(33, 64, 64), (64, 64, 64), (128, 128, 128)]:
+        blk = np.concatenate([np.array([0x00, 0x3C], np.uint8), np.full(16, 0x99, np.uint8)])
+        W = np.tile(blk, (K // 32) * N)
+        Y = oracle.gemm(0, np.ones((M, K), np.float16), W, N)
+        assert np.all(Y == K)
+
+
+def test_bridge_kat_mlx_ones(oracle):
+    # tests/test_bridge_basic.py:86-118: d = 1, bias = 0, nibbles 1 -> Y = K
+    M = K = N = 64
+    blk = np.concatenate([np.array([0x00, 0x3C, 0x00, 0x00], np.uint8), np.full(16, 0x11, np.uint8)])
+    Y = oracle.gemm(1, np.ones((M, K), np.float16), np.tile(blk, (K // 32) * N), N)
+    assert np.all(Y == K)
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+def test_gemm_matches_numpy_matmul(oracle, fmt):
+    """Oracle GEMM vs numpy float64 matmul of the (separately pinned)
+    dequantized weights: catches transposed operands, index and block-order
+    mistakes.  Both are double; outputs may differ by one fp16 ulp only where
+    the double sums straddle a rounding boundary."""
+    M, K, N = 37, 512, 96
+    X = synth.activations(M, K, 10 + fmt)
+    W = synth.random_blocks(fmt, N, K, 20 + fmt)
+    Y = oracle.gemm(fmt, X, W, N).astype(np.float64)
+    Wd = oracle.dequantize_f64(fmt, W, K, N)
+    ref = (X.astype(np.float64) @ Wd.T).astype(np.float16).astype(np.float64)
+    diff = np.abs(Y - ref)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(diff <= ulp)
+    assert np.mean(diff == 0) > 0.999
+
+
+def test_gemm_direct_head_and_residual(oracle):
+    M, K, H, D = 20, 256, 4, 64
+    N = H * D
+    X = synth.activations(M, K, 5)
+    W = synth.random_blocks(0, N, K, 6)
+    Y = oracle.gemm(0, X, W, N)
+    Yh = oracle.gemm(0, X, W, N, head_D=D)
+    # [M, N] -> [H, M, D] index map (quant_router_kernels.metal:570-574)
+    np.testing.assert_array_equal(Yh, Y.reshape(M, H, D).transpose(1, 0, 2))
+    R = synth.activations(M, N, 7)
+    Yr = oracle.gemm(0, X, W, N, R=R).astype(np.float64)
+    Wd = oracle.dequantize_f64(0, W, K, N)
+    ref = (X.astype(np.float64) @ Wd.T + R.astype(np.float64)).astype(np.float16).astype(np.float64)
+    assert np.all(np.abs(Yr - ref) <= np.spacing(np.abs(ref).astype(np.float16)))
+
+
+def test_swiglu_matches_numpy(oracle):
+    M, K, N = 9, 256, 64
+    X = synth.activations(M, K, 1)
+    Wg, Wu = synth.random_blocks(0, N, K, 2), synth.random_blocks(0, N, K, 3)
+    out = oracle.swiglu(0, X, Wg, Wu, N).astype(np.float64)
+    g = X.astype(np.float64) @ oracle.dequantize_f64(0, Wg, K, N).T
+    u = X.astype(np.float64) @ oracle.dequantize_f64(0, Wu, K, N).T
+    ref = (g / (1 + np.exp(-g)) * u).astype(np.float16).astype(np.float64)
+    assert np.all(np.abs(out - ref) <= np.spacing(np.abs(ref).astype(np.float16)))
+
+
+# --------------------------------------------------------------------------
+# Q8_0 and attention
+# --------------------------------------------------------------------------
+
+def test_q8_0_special_cases(oracle):
+    # amax = 0 -> d = 0, every code 0 (brick4_attn_bench.mm:48)
+    q = oracle.quantize_q8_0(np.zeros(32, np.float16))
+    assert np.all(q == 0)
+    # x = k * d exactly (d = 1/127 * 127 -> amax 127 gives d = 1): codes are k
+    x = np.arange(-16, 16).astype(np.float16) * np.float16(4.0)
+    x[0] = -127 * 0.5  # amax 63.5 -> d = 0.5
+    q = oracle.quantize_q8_0(x)
+    assert q[:2].copy().view(np.float16)[0] == np.float16(0.5)
+    codes = q[2:].view(np.int8)
+    np.testing.assert_array_equal(codes[1:], (np.arange(-15, 16) * 8).astype(np.int8))
+    assert codes[0] == -127
+
+
+def test_q8_0_bounds_and_rounding_brute_force(oracle):
+    """Every code is round-half-away(x / d) with the float d = amax/127, and
+    |x - q*d| <= d/2; the largest magnitude maps to +-127."""
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((500, 32)) * 10.0 ** rng.integers(-4, 3, (500, 1))).astype(np.float16)
+    q = oracle.quantize_q8_0(x).reshape(500, 34)
+    d16 = q[:, :2].copy().view(np.float16)[:, 0]
+    codes = q[:, 2:].view(np.int8).astype(np.int64)
+    xf = x.astype(np.float32)
+    amax = np.abs(xf).max(1)
+    d = (amax / np.float32(127)).astype(np.float32)
+    np.testing.assert_array_equal(d16, d.astype(np.float16))
+    assert np.all(np.abs(codes).max(1) == 127)
+    err = np.abs(xf.astype(np.float64) - codes * d[:, None].astype(np.float64))
+    assert np.all(err <= d[:, None] * 0.5 * (1 + 1e-5))
+    deq = oracle.dequantize_q8_0(q.reshape(-1)).reshape(500, 32)
+    np.testing.assert_array_equal(deq, (codes * d16[:, None].astype(np.float32)).astype(np.float16))
+
+
+def test_attention_special_cases(oracle):
+    rng = np.random.default_rng(5)
+    H, M, D = 2, 40, 64
+    V = rng.standard_normal((H, M, D)).astype(np.float16)
+    # uniform scores (Q = 0) -> O[i] = mean(V[0..i])
+    O = oracle.attention(np.zeros((H, M, D), np.float16), V, V, 0.125).astype(np.float64)
+    csum = np.cumsum(V.astype(np.float64), axis=1) / np.arange(1, M + 1)[None, :, None]
+    ref = csum.astype(np.float16).astype(np.float64)
+    # double sums in a different order: equal up to one fp16 ulp at rounding boundaries
+    assert np.all(np.abs(O - ref) <= np.spacing(np.abs(ref).astype(np.float16)))
+    assert np.mean(O == ref) > 0.99
+    # row 0 attends only to key 0 -> O[0] = V[0]
+    Q = rng.standard_normal((H, M, D)).astype(np.float16)
+    O = oracle.attention(Q, Q, V, 0.125)
+    np.testing.assert_array_equal(O[:, 0], V[:, 0])
+
+
+def test_attention_matches_numpy_and_layouts(oracle):
+    rng = np.random.default_rng(6)
+    H, M, D = 3, 50, 64
+    Q, K, V = (rng.standard_normal((H, M, D)).astype(np.float16) for _ in range(3))
+    scale = 1.0 / np.sqrt(D)
+    O = oracle.attention(Q, K, V, scale).astype(np.float64)
+    s = np.einsum("hid,hjd->hij", Q.astype(np.float64), K.astype(np.float64)) * np.float64(np.float32(scale))
+    s = np.where(np.tril(np.ones((M, M), bool))[None], s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    ref = np.einsum("hij,hjd->hid", p, V.astype(np.float64)).astype(np.float16).astype(np.float64)
+    assert np.all(np.abs(O - ref) <= np.spacing(np.abs(ref).astype(np.float16)))
+    Ot = oracle.attention(Q, K, V, scale, o_token_major=True)
+    np.testing.assert_array_equal(Ot.reshape(M, H, D).transpose(1, 0, 2), O.astype(np.float16))
+    # the Q8_0 variant is attention on the dequantized cache
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    O8 = oracle.attention_q8_0(Q, Kq, Vq, scale)
+    Kd = oracle.dequantize_q8_0(Kq).reshape(H, M, D)
+    Vd = oracle.dequantize_q8_0(Vq).reshape(H, M, D)
+    np.testing.assert_array_equal(O8, oracle.attention(Q, Kd, Vd, scale))
+
+
+def test_layer_composes_pinned_pieces(oracle):
+    rng = np.random.default_rng(7)
+    M, dm, H, D, Nm = 24, 128, 2, 64, 256
+    X = synth.activations(M, dm, 8)
+    Ws = [synth.random_blocks(0, n, k, 30 + i) for i, (n, k) in
+          enumerate([(H * D, dm)] * 3 + [(dm, H * D), (Nm, dm), (Nm, dm), (dm, Nm)])]
+    out, it = oracle.layer(0, X, *Ws, H=H, D=D, N_mlp=Nm, scale=0.125, intermediates=True)
+    q = oracle.gemm(0, X, Ws[0], H * D, head_D=D)
+    np.testing.assert_array_equal(it["Q"], q)
+    O = oracle.attention_q8_0(it["Q"], oracle.quantize_q8_0(it["K"]), oracle.quantize_q8_0(it["V"]), 0.125,
+                              o_token_major=True)
+    np.testing.assert_array_equal(it["O"], O)
+    np.testing.assert_array_equal(it["Xmid"], oracle.gemm(0, O, Ws[3], dm, R=X))
+    np.testing.assert_array_equal(it["S"], oracle.swiglu(0, it["Xmid"], Ws[4], Ws[5], Nm))
+    np.testing.assert_array_equal(out, oracle.gemm(0, it["S"], Ws[6], dm, R=it["Xmid"]))
+    assert rng is not None
