@@ -1,0 +1,310 @@
+"""Benchmark of the MI355X quantization-router prefill path.
+
+Metric: ms + effective TFLOPS per quantized projection at
+M=33/128/2048, K=4096.  One JSON line on stdout.
+
+  value         effective TFLOP/s (2*M*N*K / t) of the BASELINE headline
+                configuration configs[1]: MLX-4bit affine, M=128, K=4096,
+                N=14336 (g64 groups repacked into the router's MLX_4BIT blocks)
+  per_config    ms / TFLOP/s / GB/s and roofline fractions for every BASELINE
+                configuration (Q4_0 M=33, MLX M=128, Q4_K M=2048, ternary
+                M=129, the Llama-3.2-1B-shaped layer and its SwiGLU and
+                attention components)
+  roofline      the dominant kernel of the headline configuration, timed with
+                HIP events on the stream it runs on
+  cpu_baseline  the CPU oracle (restated reference gold path) on a bounded row
+                sample of the headline configuration, on this host's cores
+
+A step is one projection (or one layer) over one batch.  W untimed warmup
+steps run eagerly; the K timed steps are captured once into a HIP graph and
+replayed, so the timed region holds back-to-back kernels with no host launch
+gaps.  Weights rotate over enough device copies (> 512 MB) that every step
+reads them from HBM, not from the 256 MB Infinity Cache.  All inputs are
+resident in HBM before timing starts.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "m4-prefill-engine_amd"
+sys.path.insert(0, str(PKG))
+
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+ROTATE_BYTES = 512 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--configs", default="all", help="comma list of config names or 'all'")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+class Timer:
+    """Times `steps` calls of fn(i) on the current stream: eager warmup, then a
+    HIP-graph capture of the timed steps replayed between two events."""
+
+    def __init__(self, bridge, warmup: int, steps: int):
+        self.b, self.warmup, self.steps = bridge, warmup, steps
+
+    def run(self, fn) -> float:
+        import torch
+
+        s = torch.cuda.current_stream()
+        self.b.lib.m4_bridge_set_stream(s.cuda_stream)
+        for i in range(self.warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        mode = "graph"
+        g = torch.cuda.CUDAGraph()
+        try:
+            cap = torch.cuda.Stream()
+            with torch.cuda.graph(g, stream=cap):
+                self.b.lib.m4_bridge_set_stream(torch.cuda.current_stream().cuda_stream)
+                for i in range(self.steps):
+                    fn(i)
+            self.b.lib.m4_bridge_set_stream(s.cuda_stream)
+            g.replay()  # upload; untimed
+            torch.cuda.synchronize()
+        except Exception:  # capture unsupported: eager timing
+            mode = "eager"
+            self.b.lib.m4_bridge_set_stream(s.cuda_stream)
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(s)
+        if mode == "graph":
+            g.replay()
+        else:
+            for i in range(self.steps):
+                fn(i)
+        e1.record(s)
+        torch.cuda.synchronize()
+        self.mode = mode
+        return e0.elapsed_time(e1) / self.steps  # ms per step
+
+
+def rotated(t, nbytes_each: int):
+    """Device copies of t so that the set spans > ROTATE_BYTES."""
+    import torch
+
+    n = max(2, min(64, math.ceil(ROTATE_BYTES / max(1, nbytes_each))))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with status {rc}")
+
+
+def bench_projection(b, timer, name, fmt, M, K, N, seed):
+    import torch
+
+    import synth
+
+    Xn = synth.activations(M, K, seed)
+    X = torch.from_numpy(Xn).cuda()
+    Wn = synth.quantized_weights(fmt, N, K, seed + 1)
+    W0 = torch.from_numpy(Wn).cuda()
+    Ws = rotated(W0, W0.numel())
+    Y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    lib = b.lib
+    xp, yp, xb, yb = X.data_ptr(), Y.data_ptr(), X.numel() * 2, Y.numel() * 2
+    wps = [w.data_ptr() for w in Ws]
+    wb = W0.numel()
+
+    def step(i):
+        check(lib.m4_bridge_dispatch_gemm(xp, xb, wps[i % len(wps)], wb, yp, yb, fmt, M, K, N), name)
+
+    ms = timer.run(step)
+    flops = 2.0 * M * N * K
+    bytes_ = X.numel() * 2 + wb + Y.numel() * 2
+    tf = flops / (ms * 1e-3) / 1e12
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    return {
+        "name": name, "format": fmt, "M": M, "K": K, "N": N, "ms": round(ms, 5), "tflops": round(tf, 2),
+        "gbs": round(gbs, 1), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+        "flops": flops, "bytes": bytes_, "weight_copies": len(Ws), "timing": timer.mode,
+    }, (Xn, Wn)
+
+
+def bench_swiglu(b, timer, M, K, N, seed):
+    import torch
+
+    import synth
+
+    X = torch.from_numpy(synth.activations(M, K, seed)).cuda()
+    Wg = torch.from_numpy(synth.quantized_weights(0, N, K, seed + 1)).cuda()
+    Wu = torch.from_numpy(synth.quantized_weights(0, N, K, seed + 2)).cuda()
+    Out = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    lib = b.lib
+    args = (X.data_ptr(), X.numel() * 2, Wg.data_ptr(), Wg.numel(), Wu.data_ptr(), Wu.numel(), Out.data_ptr(),
+            Out.numel() * 2, 0, M, N, K)
+
+    def step(i):
+        check(lib.m4_bridge_dispatch_swiglu(*args), "swiglu")
+
+    ms = timer.run(step)
+    flops = 4.0 * M * N * K + 4.0 * M * N  # brick3_swiglu_bench.mm:489
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"name": "swiglu_q4_0", "M": M, "K": K, "N_mlp": N, "ms": round(ms, 5), "tflops": round(tf, 2),
+            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "timing": timer.mode}
+
+
+def bench_attention(b, timer, H, M, D, seed):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    Q = torch.from_numpy(rng.standard_normal((H, M, D)).astype(np.float16)).cuda()
+    Kf = torch.from_numpy(rng.standard_normal((H, M, D)).astype(np.float16)).cuda()
+    Vf = torch.from_numpy(rng.standard_normal((H, M, D)).astype(np.float16)).cuda()
+    nb = H * M * D // 32
+    Kq = torch.empty(nb * 34, dtype=torch.uint8, device="cuda")
+    Vq = torch.empty(nb * 34, dtype=torch.uint8, device="cuda")
+    lib = b.lib
+    check(lib.m4_bridge_quantize_kv_q8_0(Kf.data_ptr(), Kf.numel() * 2, Kq.data_ptr(), Kq.numel(), nb), "q8")
+    check(lib.m4_bridge_quantize_kv_q8_0(Vf.data_ptr(), Vf.numel() * 2, Vq.data_ptr(), Vq.numel(), nb), "q8")
+    O = torch.empty(H, M, D, dtype=torch.float16, device="cuda")
+    args = (Q.data_ptr(), Q.numel() * 2, Kq.data_ptr(), Kq.numel(), Vq.data_ptr(), Vq.numel(), O.data_ptr(),
+            O.numel() * 2, H, M, D, 1.0 / math.sqrt(D), 0)
+
+    def step(i):
+        check(lib.m4_bridge_dispatch_flash_attn_q8_0(*args), "attention")
+
+    ms = timer.run(step)
+    flops = 2.0 * H * M * (M + 1) * D  # brick4_attn_bench.mm:475
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"name": "flash_attn_q8_0", "H": H, "M": M, "D": D, "ms": round(ms, 5), "tflops": round(tf, 2),
+            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "timing": timer.mode}
+
+
+def bench_layer(b, timer, M, dm, H, D, Nm, seed):
+    import torch
+
+    import synth
+
+    X = torch.from_numpy(synth.activations(M, dm, seed)).cuda()
+    shapes = [(H * D, dm)] * 3 + [(dm, H * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    Ws = [torch.from_numpy(synth.quantized_weights(0, n, k, seed + 1 + i)).cuda() for i, (n, k) in enumerate(shapes)]
+    Xo = torch.empty(M, dm, dtype=torch.float16, device="cuda")
+    lib = b.lib
+    ptrs = [X.data_ptr()] + [w.data_ptr() for w in Ws] + [Xo.data_ptr()]
+
+    def step(i):
+        check(lib.m4_bridge_prefill_layer(*ptrs, 0, M, dm, H, D, Nm, 1.0 / math.sqrt(D)), "layer")
+
+    ms = timer.run(step)
+    HD = H * D
+    flops = 2.0 * M * dm * HD * 4 + 2.0 * M * dm * Nm * 3 + 2.0 * H * M * (M + 1) * D
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"name": "layer_llama32_1b_q4_0_q8kv", "M": M, "d_model": dm, "H": H, "D": D, "N_mlp": Nm,
+            "ms": round(ms, 5), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4),
+            "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
+
+
+def cpu_baseline(fmt, X, Wn, N, seconds: float):
+    """The oracle (CPU restatement of the reference's gold) on a growing row
+    sample of the headline configuration until ~`seconds` of CPU work."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle_bindings as ob
+
+    threads = ob.threads()
+    M, K = X.shape
+    rows, t_total, done = 1, 0.0, 0
+    while done < M and t_total < seconds:
+        r = min(rows, M - done)
+        t0 = time.perf_counter()
+        ob.gemm(fmt, X[done:done + r], Wn, N, nthreads=threads)
+        t_total += time.perf_counter() - t0
+        done += r
+        rows *= 2
+    tf = 2.0 * done * N * K / t_total / 1e12
+    return {"value": round(tf, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of {M} rows of the headline projection (M={M}, K={K}, N={N}), "
+                      f"{t_total:.1f} s, double accumulation, one task per row",
+            "ms_full_projection_est": round(t_total / done * M * 1e3, 1)}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
+                                   "design-only, see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    import m4_bridge
+
+    b = m4_bridge.HIPBridge.get_instance(PKG / "libm4_bridge.so")
+    assert b.init(), b.last_error()
+    timer = Timer(b, a.warmup, a.steps)
+    want = None if a.configs == "all" else set(a.configs.split(","))
+
+    def on(name):
+        return want is None or name in want
+
+    per = {}
+    head_inputs = None
+    if on("cfg2_mlx_m128"):
+        per["cfg2_mlx_m128"], head_inputs = bench_projection(b, timer, "cfg2_mlx_m128", 1, 128, 4096, 14336, 20)
+    if on("cfg1_q4_0_m33"):
+        per["cfg1_q4_0_m33"], _ = bench_projection(b, timer, "cfg1_q4_0_m33", 0, 33, 4096, 4096, 10)
+    if on("cfg3_q4_k_m2048"):
+        per["cfg3_q4_k_m2048"], _ = bench_projection(b, timer, "cfg3_q4_k_m2048", 2, 2048, 4096, 4096, 30)
+    if on("cfg4_ternary_m129"):
+        per["cfg4_ternary_m129"], _ = bench_projection(b, timer, "cfg4_ternary_m129", 3, 129, 2048, 8192, 40)
+    for fmt, tag in ((0, "q4_0"), (1, "mlx"), (3, "ternary")):
+        name = f"m2048_k4096_{tag}"
+        if want is not None and name in want:
+            per[name], _ = bench_projection(b, timer, name, fmt, 2048, 4096, 4096, 60 + fmt)
+    if on("cfg5_swiglu"):
+        per["cfg5_swiglu"] = bench_swiglu(b, timer, 2048, 2048, 8192, 50)
+    if on("cfg5_attention"):
+        per["cfg5_attention"] = bench_attention(b, timer, 32, 2048, 64, 51)
+    if on("cfg5_layer"):
+        per["cfg5_layer"] = bench_layer(b, timer, 2048, 2048, 32, 64, 8192, 52)
+
+    head = per.get("cfg2_mlx_m128") or next(iter(per.values()))
+    out = {
+        "metric": "ms + effective TFLOPS per quantized projection at M=33/128/2048, K=4096",
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (4-bit weights dequantized to fp16, fp32 accumulate)",
+        "data": "synthetic: seeded N(0,1) activations, N(0,0.02) weights quantized per BASELINE configs",
+        "config": {"workload": "MLX-4bit affine projection M=128 K=4096 N=14336 (BASELINE configs[1])",
+                   "M": 128, "K": 4096, "N": 14336, "format": "MLX_4BIT (g64 repacked to 32-blocks)"},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_kernel<QUANT_MLX_4BIT>", "hbm_frac": head.get("frac_hbm")},
+        "per_config": per,
+    }
+    if not a.no_cpu_baseline and head_inputs is not None:
+        X, Wn = head_inputs
+        out["cpu_baseline"] = cpu_baseline(1, X, Wn, 14336, a.cpu_seconds)
+    b.synchronize()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()
