@@ -249,7 +249,7 @@ def main():
 
     import m4_bridge
 
-    b = m4_bridge.HIPBridge.get_instance(PKG / "libm4_bridge.so")
+    b = m4_bridge.HIPBridge.get_instance(os.environ.get("M4_BRIDGE_LIB_PATH") or PKG / "libm4_bridge.so")
     assert b.init(), b.last_error()
     timer = Timer(b, a.warmup, a.steps)
     want = None if a.configs == "all" else set(a.configs.split(","))

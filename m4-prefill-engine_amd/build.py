@@ -17,7 +17,7 @@ OUT = HERE / "libm4_bridge.so"
 BUILD = HERE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["qr_gemm.hip", "qr_attention.hip", "qr_bridge.cpp", "qr_registry.cpp"]
+SOURCES = ["qr_gemm.hip", "qr_gemm_skinny.hip", "qr_attention.hip", "qr_bridge.cpp", "qr_registry.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-ffp-contract=on",
           "-fvisibility=hidden", "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
@@ -27,28 +27,31 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-ffp-contract=
 DEVICE = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def _compile(src: str) -> Path:
-    obj = BUILD / (Path(src).stem + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(src: str, build_dir: Path = BUILD, extra: tuple = ()) -> Path:
+    obj = build_dir / (Path(src).stem + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
-        cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {src}\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     return obj
 
 
-def build(jobs: int = 4, verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int = 4, verbose: bool = False, out: Path = OUT, build_dir: Path = BUILD,
+          extra: tuple = ()) -> Path:
+    """Compile every source (optionally with extra compiler flags, e.g. -D
+    tuning macros) and link `out`."""
+    build_dir.mkdir(parents=True, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", str(OUT), *map(str, objs)]
+        objs = list(ex.map(lambda s: _compile(s, build_dir, tuple(extra)), SOURCES))
+    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", str(out), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     if verbose:
-        print(f"built {OUT}")
-    return OUT
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":

@@ -134,7 +134,56 @@ int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, 
     return 0;
 }
 
+// Split-K workspace of the small-M kernel: grow-only, counters zeroed once at
+// allocation and left zeroed by every launch.
+float* g_sk_ws = nullptr;
+size_t g_sk_ws_floats = 0;
+uint32_t* g_sk_cnt = nullptr;
+size_t g_sk_cnt_n = 0;
+
+hipError_t ensure_skinny_ws(size_t floats, size_t groups) {
+    if (floats > g_sk_ws_floats) {
+        if (g_sk_ws) {
+            (void)hipStreamSynchronize(g_stream);
+            (void)hipFree(g_sk_ws);
+        }
+        g_sk_ws = nullptr;
+        g_sk_ws_floats = 0;
+        hipError_t e = hipMalloc(&g_sk_ws, floats * sizeof(float));
+        if (e != hipSuccess) return e;
+        g_sk_ws_floats = floats;
+    }
+    if (groups > g_sk_cnt_n) {
+        if (g_sk_cnt) {
+            (void)hipStreamSynchronize(g_stream);
+            (void)hipFree(g_sk_cnt);
+        }
+        g_sk_cnt = nullptr;
+        g_sk_cnt_n = 0;
+        hipError_t e = hipMalloc(&g_sk_cnt, groups * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemset(g_sk_cnt, 0, groups * sizeof(uint32_t));
+        if (e != hipSuccess) return e;
+        g_sk_cnt_n = groups;
+    }
+    return hipSuccess;
+}
+
 int launch(const qr::GemmParams& p) {
+    if (qr::skinny_supported(p)) {
+        uint32_t ks = 0, groups = 0;
+        size_t floats = qr::skinny_workspace_floats(p.M, p.N, p.K, &ks, &groups);
+        hipError_t e = ensure_skinny_ws(floats ? floats : 1, groups);
+        if (e != hipSuccess) {
+            set_error("hipMalloc(split-K workspace)", e);
+            return -5;
+        }
+        e = qr::launch_gemm_skinny(p, g_sk_ws, g_sk_cnt, g_stream);
+        if (e != hipSuccess) {
+            set_error("launch_gemm_skinny", e);
+            return -6;
+        }
+        return 0;
+    }
     hipError_t e = qr::launch_gemm(p, g_stream);
     if (e != hipSuccess) {
         set_error("launch_gemm", e);
@@ -422,7 +471,7 @@ double m4_bridge_get_uma_footprint_mb(void) {
         fclose(f);
     }
     double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
-    return host_mb + (double)(g_ws_bytes + g_staged_bytes) / (1024.0 * 1024.0);
+    return host_mb + (double)(g_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 + g_sk_cnt_n * 4) / (1024.0 * 1024.0);
 }
 
 bool m4_bridge_is_initialized(void) {
@@ -437,6 +486,11 @@ void m4_bridge_shutdown(void) {
     if (g_ws) (void)hipFree(g_ws);
     g_ws = nullptr;
     g_ws_bytes = 0;
+    if (g_sk_ws) (void)hipFree(g_sk_ws);
+    if (g_sk_cnt) (void)hipFree(g_sk_cnt);
+    g_sk_ws = nullptr;
+    g_sk_cnt = nullptr;
+    g_sk_ws_floats = g_sk_cnt_n = 0;
     if (g_own_stream) (void)hipStreamDestroy(g_own_stream);
     g_own_stream = nullptr;
     g_stream = nullptr;

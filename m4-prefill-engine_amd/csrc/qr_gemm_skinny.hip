@@ -1,0 +1,514 @@
+// qr_gemm_skinny.hip -- weight-streaming projection for small M (M <= 64).
+//
+// The M=33 prefill projection is bound by streaming the
+// packed weights from HBM; the reference's 64x64 tiling (quant_router_kernels.
+// metal:442-581) leaves 31 of 64 rows idle and launches only N/64 groups.
+// Here every CU streams its own slice of W:
+//  * a workgroup = 8 wave64s owns 64 output columns and a K range of KC
+//    elements; the K range is split across KSPLIT workgroups so the grid
+//    covers the 256 CUs;
+//  * load phase: the workgroup's 64 weight strips (one contiguous byte range
+//    per column) and its activation rows (M x KC fp16) are copied to LDS with
+//    fully coalesced 16-byte buffer loads -- every wave keeps its whole share
+//    in flight at once; strips and rows are padded by 16 bytes so the
+//    fragment reads below spread over the LDS banks;
+//  * compute phase: wave w takes groups [w*GPW, (w+1)*GPW) of the range.
+//    Weights are the A operand of v_mfma_f32_16x16x32_f16 (16 columns x one
+//    32-element quant group): each lane reads the raw bytes of its 8 elements
+//    from LDS and decodes them to binary16 in registers (bit-exact vs the CPU
+//    unpack); activations are the B operand, 16 rows per tile, reused across
+//    the wave's 4 column tiles;
+//  * partial sums: the 8 waves reduce through LDS in a fixed order; KSPLIT
+//    workgroups of one column group write fp32 partials to a workspace with
+//    agent-scope stores and the last to arrive (agent-scope counter) sums them
+//    in split order, rounds once to fp16 and resets the counter --
+//    deterministic, one launch, no L2 writeback/invalidate.
+#include "qr_device.h"
+#include "qr_formats.h"
+#include "qr_kernels.h"
+
+namespace qr {
+
+__device__ __forceinline__ uint32_t lds32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// A-operand fragment of one 32-element group, read from a weight strip in LDS
+// (16-byte aligned).  Lane group g = lane / 16 holds elements 8g .. 8g+7.
+// load() reads the raw words of one lane from LDS; decode() is lane-local.
+template <int F> struct Frag;
+
+// Q4_0: elements 8g..8g+7 are the low (g < 2) or high (g >= 2) nibbles of
+// code bytes 8(g&1) .. 8(g&1)+7, read as three aligned dwords plus a byte
+// funnel shift (18-byte groups are only 2-byte aligned), and the dword that
+// holds the scale.
+template <> struct Frag<QUANT_Q4_0> {
+    static constexpr int kRaw = 4;
+    __device__ static uint32_t start(uint32_t kb, int g) { return kb * 18u + ((g & 1) ? 10u : 0u); }
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[4]) {
+        const uint8_t* p = strip + (start(kb, g) & ~3u);
+        raw[0] = lds32(p); raw[1] = lds32(p + 4); raw[2] = lds32(p + 8);
+        raw[3] = lds32(strip + ((kb * 18u) & ~3u));  // dword holding the scale
+    }
+    __device__ static h8_t decode(const uint32_t raw[4], uint32_t kb, int g) {
+        const uint32_t sh = start(kb, g) & 2u;
+        const uint32_t v0 = sh ? __builtin_amdgcn_alignbyte(raw[1], raw[0], 2) : raw[0];
+        const uint32_t v1 = sh ? __builtin_amdgcn_alignbyte(raw[2], raw[1], 2) : raw[1];
+        const uint32_t v2 = sh ? (raw[2] >> 16) : raw[2];
+        uint32_t q0, q1;
+        if (g & 1) {
+            q0 = v0; q1 = v1;
+        } else {
+            q0 = __builtin_amdgcn_alignbyte(v1, v0, 2);
+            q1 = __builtin_amdgcn_alignbyte(v2, v1, 2);
+        }
+        const uint32_t d16 = ((kb * 18u) & 2u) ? (raw[3] >> 16) : (raw[3] & 0xffffu);
+        if (g >= 2) { q0 >>= 4; q1 >>= 4; }
+        q0 &= 0x0f0f0f0fu;
+        q1 &= 0x0f0f0f0fu;
+        const h2_t d = as_h2(d16 | (d16 << 16));
+        const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+        u4_t w = {as_u32((as_h2(nib_pair_lo(q0)) - off) * d), as_u32((as_h2(nib_pair_hi(q0)) - off) * d),
+                  as_u32((as_h2(nib_pair_lo(q1)) - off) * d), as_u32((as_h2(nib_pair_hi(q1)) - off) * d)};
+        return __builtin_bit_cast(h8_t, w);
+    }
+};
+
+// MLX_4BIT (20-byte groups, dword aligned): every lane reads {d, bias} and
+// its two code dwords (codes 0..7 for g&1 == 0, 8..15 for g&1 == 1).
+template <> struct Frag<QUANT_MLX_4BIT> {
+    static constexpr int kRaw = 3;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[3]) {
+        // raw = {d | bias, code dwords 2(g&1), 2(g&1)+1}
+        const uint8_t* p = strip + kb * 20u;
+        raw[0] = lds32(p);
+        raw[1] = lds32(p + 4u + 8u * (uint32_t)(g & 1));
+        raw[2] = lds32(p + 8u + 8u * (uint32_t)(g & 1));
+    }
+    __device__ static h8_t decode(const uint32_t raw[3], uint32_t, int g) {
+        const uint32_t db = raw[0];
+        uint32_t q0 = raw[1];
+        uint32_t q1 = raw[2];
+        if (g >= 2) { q0 >>= 4; q1 >>= 4; }
+        q0 &= 0x0f0f0f0fu;
+        q1 &= 0x0f0f0f0fu;
+        const uint32_t d16 = db & 0xffffu, b16 = db >> 16;
+        const h2_t d = as_h2(d16 | (d16 << 16)), bias = as_h2(b16 | (b16 << 16));
+        const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
+        u4_t w = {as_u32(__builtin_elementwise_fma(as_h2(nib_pair_lo(q0)) - off, d, bias)),
+                  as_u32(__builtin_elementwise_fma(as_h2(nib_pair_hi(q0)) - off, d, bias)),
+                  as_u32(__builtin_elementwise_fma(as_h2(nib_pair_lo(q1)) - off, d, bias)),
+                  as_u32(__builtin_elementwise_fma(as_h2(nib_pair_hi(q1)) - off, d, bias))};
+        return __builtin_bit_cast(h8_t, w);
+    }
+};
+
+// Q4_K: group kb is sub-block s = kb % 8 of super-block kb / 8.  Every lane
+// reads the 16-byte header and its 8 code bytes 16s + 8(g&1) .. +7.
+template <> struct Frag<QUANT_Q4_K> {
+    static constexpr int kRaw = 6;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[6]) {
+        const uint8_t* p = strip + (kb >> 3) * 144u;
+        u4_t h = *reinterpret_cast<const u4_t*>(p);
+        u2_t q = *reinterpret_cast<const u2_t*>(p + 16u + 16u * (kb & 7u) + 8u * (uint32_t)(g & 1));
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w; raw[4] = q.x; raw[5] = q.y;
+    }
+    __device__ static int binade(uint32_t h16) {
+        int e = (int)((h16 >> 10) & 0x1f);
+        return (e < 1 ? 1 : e) - 15;
+    }
+    __device__ static h8_t decode(const uint32_t raw[6], uint32_t kb, int g) {
+        const uint32_t s = kb & 7u;
+        const uint32_t d16 = raw[0] & 0xffffu, dm16 = raw[0] >> 16;
+        const uint64_t s07 = (uint64_t)raw[1] | ((uint64_t)raw[2] << 32);
+        const uint32_t scj = (uint32_t)(s07 >> (8u * s)) & 0xffu;
+        const uint32_t sc = scj & 63u;
+        const uint32_t lowm = (s < 4) ? ((raw[3] >> (8u * s)) & 0x0fu) : ((raw[3] >> (8u * (s - 4u) + 4u)) & 0x0fu);
+        const uint32_t mn = lowm | ((scj >> 6) << 4);
+        const float A = h2f(d16) * (float)sc;
+        const float B = h2f(dm16) * (float)mn;
+        const int gap = binade(d16) - binade(dm16);
+        const bool fast = (A == 0.0f) || (B == 0.0f) || (gap <= 3 && gap >= -7);
+        uint32_t q0 = raw[4], q1 = raw[5];
+        if (g >= 2) { q0 >>= 4; q1 >>= 4; }
+        q0 &= 0x0f0f0f0fu;
+        q1 &= 0x0f0f0f0fu;
+        uint32_t v[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float c0 = (float)((q0 >> (8 * i)) & 0xffu), c1 = (float)((q1 >> (8 * i)) & 0xffu);
+            v[i] = fast ? f2h_bits(__builtin_fmaf(c0, A, -B)) : rne16_sum(c0 * A, -B);
+            v[4 + i] = fast ? f2h_bits(__builtin_fmaf(c1, A, -B)) : rne16_sum(c1 * A, -B);
+        }
+        u4_t w = {pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7])};
+        return __builtin_bit_cast(h8_t, w);
+    }
+};
+
+// TERNARY_1_58 (12-byte groups): elements 8g..8g+7 are the 16-bit field
+// 16(g&1) of code word g/2.  w = (1024 + c - 1025) * d, exact.
+template <> struct Frag<QUANT_TERNARY_1_58> {
+    static constexpr int kRaw = 2;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
+        const uint8_t* p = strip + kb * 12u;
+        raw[0] = lds32(p);
+        raw[1] = lds32(p + 4u + 4u * (uint32_t)(g >> 1));
+    }
+    __device__ static h8_t decode(const uint32_t raw[2], uint32_t, int g) {
+        const uint32_t d16 = raw[0] & 0xffffu;
+        const uint32_t c = (raw[1] >> (16 * (g & 1))) & 0xffffu;
+        const h2_t d = as_h2(d16 | (d16 << 16));
+        const h2_t off = {(_Float16)1025.0f, (_Float16)1025.0f};
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t t = (c >> (4 * i)) & 0xfu;
+            const uint32_t pr = (t & 3u) | ((t >> 2) << 16) | 0x64006400u;
+            w[i] = as_u32((as_h2(pr) - off) * d);
+        }
+        return __builtin_bit_cast(h8_t, u4_t{w[0], w[1], w[2], w[3]});
+    }
+};
+
+#ifdef QR_SK_TRACE
+__device__ unsigned long long qr_sk_trace[65536];
+#define SK_TRACE(k)                                                                             \
+    do {                                                                                       \
+        if (threadIdx.x == 0)                                                                  \
+            qr_sk_trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + (k)] =               \
+                __builtin_amdgcn_s_memrealtime();                                              \
+    } while (0)
+#else
+#define SK_TRACE(k) ((void)0)
+#endif
+
+constexpr int kSkWaves = 8;
+constexpr int kSkNT = 4;                  // 16-column tiles per wave
+constexpr int kSkCols = 16 * kSkNT;       // columns per workgroup
+constexpr uint32_t kSkLdsMax = 159 * 1024;  // 160 KB LDS less static allocations
+
+// Bytes of one 32-element group of format F.
+template <int F> struct GroupBytes;
+template <> struct GroupBytes<QUANT_Q4_0> { static constexpr uint32_t v = 18; };
+template <> struct GroupBytes<QUANT_MLX_4BIT> { static constexpr uint32_t v = 20; };
+template <> struct GroupBytes<QUANT_Q4_K> { static constexpr uint32_t v = 18; };  // 144 / 8
+template <> struct GroupBytes<QUANT_TERNARY_1_58> { static constexpr uint32_t v = 12; };
+
+// LDS layout of one launch: activation rows [M][KC*2 + 16 bytes], then 64
+// weight strips [64][SB + 16 bytes]; the wave reduction reuses it from 0.
+struct SkLayout {
+    uint32_t xrs, sb, sbp, x_bytes, lds;
+};
+__host__ __device__ inline SkLayout sk_layout(uint32_t M, uint32_t gpw, uint32_t group_bytes) {
+    SkLayout L;
+    const uint32_t kc = gpw * kSkWaves * 32;
+    L.xrs = kc * 2 + 16;
+    L.sb = gpw * kSkWaves * group_bytes;
+    L.sbp = L.sb + 16;
+    L.x_bytes = M * L.xrs;
+    const uint32_t mt = (M + 15) / 16;
+    const uint32_t red = kSkWaves * mt * 16 * (kSkCols + 4) * 4;
+    const uint32_t load = L.x_bytes + kSkCols * L.sbp;
+    L.lds = load > red ? load : red;
+    return L;
+}
+
+template <int F, int MT, int GPW>  // MT: 16-row tiles of M; GPW: 32-groups per wave
+__global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* ws, uint32_t* counters,
+                                                          uint32_t ksplit) {
+    using FR = Frag<F>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr uint32_t GB = GroupBytes<F>::v;
+    constexpr uint32_t KC = GPW * kSkWaves * 32;      // K elements of this workgroup
+    constexpr uint32_t SB = GPW * kSkWaves * GB;      // strip bytes (multiple of 16)
+    static_assert(SB % 16 == 0, "strip bytes must be a multiple of 16");
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r16 = lane & 15;
+    const uint32_t cg = blockIdx.x, ks = blockIdx.y;
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t n0 = cg * kSkCols;
+    const uint32_t col_bytes = (uint32_t)p.col_bytes;
+    const uint32_t ncols = min((uint32_t)kSkCols, N - n0);
+    const SkLayout L = sk_layout(M, GPW, GB);
+    uint8_t* xs = smem;
+    uint8_t* wsb = smem + L.x_bytes;
+
+    SK_TRACE(0);
+    // ---- load phase: strips and rows to LDS, all loads in flight ----
+    {
+        auto wr = make_rsrc(p.W + (size_t)n0 * col_bytes, ncols * col_bytes);
+        auto xr = make_rsrc(p.X, M * K * 2u);
+        constexpr uint32_t WCH = kSkCols * SB / 16;       // 16-byte chunks of the strips
+        constexpr uint32_t WPT = (WCH + 511) / 512;
+        constexpr uint32_t xch_row = KC * 2 / 16;
+        const uint32_t XCH = M * xch_row;
+        constexpr uint32_t XPT_MAX = (MT * 16 * xch_row + 511) / 512;
+        u4_t wv[WPT], xv[XPT_MAX];
+#pragma unroll
+        for (uint32_t i = 0; i < WPT; i++) {
+            const uint32_t q = tid + 512 * i;
+            const uint32_t c = q / (SB / 16), j = q % (SB / 16);
+            const uint32_t off = (q < WCH && c < ncols) ? c * col_bytes + ks * SB + 16 * j : kOOB;
+            wv[i] = ld_b128(wr, off);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < XPT_MAX; i++) {
+            const uint32_t q = tid + 512 * i;
+            const uint32_t m = q / xch_row, j = q % xch_row;
+            const uint32_t off = (q < XCH) ? (m * K + ks * KC) * 2u + 16 * j : kOOB;
+            xv[i] = ld_b128(xr, off);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < WPT; i++) {
+            const uint32_t q = tid + 512 * i;
+            if (q < WCH) *reinterpret_cast<u4_t*>(wsb + (q / (SB / 16)) * L.sbp + 16 * (q % (SB / 16))) = wv[i];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < XPT_MAX; i++) {
+            const uint32_t q = tid + 512 * i;
+            if (q < XCH) *reinterpret_cast<u4_t*>(xs + (q / xch_row) * L.xrs + 16 * (q % xch_row)) = xv[i];
+        }
+    }
+    __syncthreads();
+    SK_TRACE(1);
+
+    // ---- compute phase: acc[t][mt] rows n = 16t + 4g + i, column m = 16mt + r16 ----
+    f4_t acc[kSkNT][MT];
+#pragma unroll
+    for (int t = 0; t < kSkNT; t++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[t][mt] = f4_t{};
+    // All LDS reads of the wave first (one latency), then decode + MFMA.
+    uint32_t raw[GPW][kSkNT][FR::kRaw];
+    u4_t xf[GPW][MT];
+#pragma unroll
+    for (int b = 0; b < GPW; b++) {
+        const uint32_t kb = wave * GPW + b;  // group within the workgroup's range
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const uint32_t m = min(16u * mt + r16, M - 1);  // rows >= M are zeroed below
+            xf[b][mt] = *reinterpret_cast<const u4_t*>(xs + m * L.xrs + (kb * 32u + 8u * g) * 2u);
+        }
+#pragma unroll
+        for (int t = 0; t < kSkNT; t++) FR::load(wsb + (16u * t + r16) * L.sbp, kb, g, raw[b][t]);
+    }
+#pragma unroll
+    for (int b = 0; b < GPW; b++) {
+        const uint32_t kb = wave * GPW + b;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            if (16u * mt + r16 >= M) xf[b][mt] = u4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < kSkNT; t++) {
+            const h8_t a = FR::decode(raw[b][t], kb, g);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, xf[b][mt]),
+                                                                   acc[t][mt], 0, 0, 0);
+        }
+    }
+    SK_TRACE(2);
+
+    // ---- reduce the 8 waves through LDS (fixed order) ----
+    // Per-wave buffer [m][n] with row stride RS = 64 + 4 floats: a lane's four
+    // accumulator rows are 4 consecutive n, stored with one ds_write_b128; the
+    // summing pass reads consecutive n (conflict-free) and the outputs leave
+    // in row-major order.
+    constexpr int ROWS = MT * 16;
+    constexpr int RS = kSkCols + 4;
+    float* red = reinterpret_cast<float*>(smem);
+    __syncthreads();  // every wave is done reading the staged operands
+    float* mine = red + wave * ROWS * RS;
+#pragma unroll
+    for (int t = 0; t < kSkNT; t++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            *reinterpret_cast<f4_t*>(mine + (16 * mt + r16) * RS + 16 * t + 4 * g) = acc[t][mt];
+    __syncthreads();
+
+    const bool split = ksplit > 1;
+    __shared__ uint32_t s_last;
+    constexpr int NEL = ROWS * kSkCols;
+    constexpr int PER = (NEL + 511) / 512;  // outputs per thread; element idx -> (m = idx / 64, n = idx % 64)
+    float tot[PER];
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int idx = tid + 512 * e;
+        const int off = (idx / kSkCols) * RS + idx % kSkCols;
+        float s = 0.0f;
+        if (idx < NEL) {
+#pragma unroll
+            for (int w = 0; w < kSkWaves; w++) s += red[w * ROWS * RS + off];
+        }
+        tot[e] = s;
+    }
+
+    auto emit = [&](int idx, float v) {
+        const uint32_t m = idx / kSkCols, nl = idx % kSkCols;
+        const uint32_t n = n0 + nl;
+        if (idx < NEL && m < M && nl < ncols) {
+            if (p.R) v += (float)p.R[(size_t)m * N + n];
+            size_t o;
+            if (p.head_D) {
+                const uint32_t h = n / p.head_D, dd = n % p.head_D;
+                o = ((size_t)h * M + m) * p.head_D + dd;
+            } else {
+                o = (size_t)m * N + n;
+            }
+            p.Y[o] = (_Float16)v;
+        }
+    };
+
+    SK_TRACE(3);
+    if (!split) {
+#pragma unroll
+        for (int e = 0; e < PER; e++) emit(tid + 512 * e, tot[e]);
+        return;
+    }
+
+    // ---- cross-workgroup split-K: partial slot ks, last arriver sums ----
+    // Partials are written with agent-scope atomic stores (coherent across
+    // XCDs without dirtying L2), so publishing them needs only the completion
+    // wait before the counter update -- no L2 writeback or invalidate, which
+    // would evict the operands every other workgroup on the XCD re-reads.
+    float* slot = ws + ((size_t)ks * gridDim.x + cg) * NEL;
+#pragma unroll
+    for (int e = 0; e < PER; e++)
+        if (tid + 512 * e < NEL)
+            __hip_atomic_store(slot + tid + 512 * e, tot[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
+    __syncthreads();
+    SK_TRACE(4);
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(counters + cg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == ksplit - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    SK_TRACE(5);
+    if (!s_last) return;
+    // Sum the split partials in split order; four splits' loads are issued
+    // together (indices clamped, not branched) so their latencies overlap.
+    static_assert(NEL % 512 == 0, "whole rows of outputs per thread");
+    float sum[PER];
+#pragma unroll
+    for (int e = 0; e < PER; e++) sum[e] = 0.0f;
+    for (uint32_t k0 = 0; k0 < ksplit; k0 += 4) {
+        float v[4][PER];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t k2 = min(k0 + j, ksplit - 1);
+            const float* src = ws + ((size_t)k2 * gridDim.x + cg) * NEL + tid;
+#pragma unroll
+            for (int e = 0; e < PER; e++)
+                v[j][e] = __hip_atomic_load(src + 512 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < PER; e++) sum[e] += (k0 + j < ksplit) ? v[j][e] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < PER; e++) emit(tid + 512 * e, sum[e]);
+    if (tid == 0) __hip_atomic_store(counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    SK_TRACE(6);
+}
+
+static uint32_t group_bytes_rt(int f) {
+    switch (f) {
+        case QUANT_Q4_0: return GroupBytes<QUANT_Q4_0>::v;
+        case QUANT_MLX_4BIT: return GroupBytes<QUANT_MLX_4BIT>::v;
+        case QUANT_Q4_K: return GroupBytes<QUANT_Q4_K>::v;
+        case QUANT_TERNARY_1_58: return GroupBytes<QUANT_TERNARY_1_58>::v;
+        default: return 0;
+    }
+}
+
+// Split selection: 4, 2 or 1 groups per wave (K range 1024, 512 or 256 per
+// workgroup); the longest range that still gives >= 256 workgroups, fits LDS
+// and needs at most 16 splits.
+static bool sk_plan(int f, uint32_t M, uint32_t N, uint32_t K, uint32_t* ks_out, uint32_t* gpw_out) {
+    const uint32_t gb = group_bytes_rt(f);
+    if (!gb || M == 0 || M > 64 || K % 256) return false;
+    const uint32_t groups = (N + kSkCols - 1) / kSkCols;
+    const uint32_t ng = K / 32;
+    for (uint32_t gpw : {4u, 2u, 1u}) {
+        if (ng % (gpw * kSkWaves)) continue;
+        const uint32_t ks = ng / (gpw * kSkWaves);
+        if (ks > 16) continue;
+        if (groups * ks < 256 && gpw > 1) continue;
+        if (sk_layout(M, gpw, gb).lds > kSkLdsMax) continue;
+        *ks_out = ks;
+        *gpw_out = gpw;
+        return true;
+    }
+    return false;
+}
+
+size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K, uint32_t* ksplit_out, uint32_t* groups_out) {
+    uint32_t ks_max = 1;
+    for (int f = 0; f < 4; f++) {
+        uint32_t ks = 1, gpw = 1;
+        if (sk_plan(f, M, N, K, &ks, &gpw) && ks > ks_max) ks_max = ks;
+    }
+    const uint32_t groups = (N + kSkCols - 1) / kSkCols;
+    if (ksplit_out) *ksplit_out = ks_max;
+    if (groups_out) *groups_out = groups;
+    return ks_max > 1 ? (size_t)ks_max * groups * ((M + 15) / 16) * 16 * kSkCols : 0;
+}
+
+template <int F, int MT, int GPW>
+static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t* counters, uint32_t ks, hipStream_t st) {
+    auto kern = gemm_skinny_kernel<F, MT, GPW>;
+    const uint32_t groups = (p.N + kSkCols - 1) / kSkCols;
+    const size_t lds = sk_layout(p.M, GPW, GroupBytes<F>::v).lds;
+    static size_t attr = 0;  // dynamic LDS limit set for this instantiation
+    if (lds > attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = lds;
+    }
+    hipLaunchKernelGGL(kern, dim3(groups, ks), dim3(512), lds, st, p, ws, counters, ks);
+    return hipGetLastError();
+}
+
+template <int F, int MT>
+static hipError_t launch_sk_g(const GemmParams& p, float* ws, uint32_t* counters, uint32_t ks, uint32_t gpw,
+                              hipStream_t st) {
+    switch (gpw) {
+        case 1: return launch_sk<F, MT, 1>(p, ws, counters, ks, st);
+        case 2: return launch_sk<F, MT, 2>(p, ws, counters, ks, st);
+        case 4: return launch_sk<F, MT, 4>(p, ws, counters, ks, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int F>
+static hipError_t launch_sk_m(const GemmParams& p, float* ws, uint32_t* counters, hipStream_t st) {
+    uint32_t ks = 0, gpw = 0;
+    if (!sk_plan(F, p.M, p.N, p.K, &ks, &gpw)) return hipErrorInvalidValue;
+    switch ((p.M + 15) / 16) {
+        case 1: return launch_sk_g<F, 1>(p, ws, counters, ks, gpw, st);
+        case 2: return launch_sk_g<F, 2>(p, ws, counters, ks, gpw, st);
+        case 3: return launch_sk_g<F, 3>(p, ws, counters, ks, gpw, st);
+        case 4: return launch_sk_g<F, 4>(p, ws, counters, ks, gpw, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool skinny_supported(const GemmParams& p) {
+    if (p.W2 || p.format < 0 || p.format > 3) return false;
+    if (p.col_bytes % 16) return false;
+    uint32_t ks, gpw;
+    return sk_plan(p.format, p.M, p.N, p.K, &ks, &gpw);
+}
+
+hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, uint32_t* counters, hipStream_t st) {
+    switch (p.format) {
+        case QUANT_Q4_0: return launch_sk_m<QUANT_Q4_0>(p, ws, counters, st);
+        case QUANT_MLX_4BIT: return launch_sk_m<QUANT_MLX_4BIT>(p, ws, counters, st);
+        case QUANT_Q4_K: return launch_sk_m<QUANT_Q4_K>(p, ws, counters, st);
+        case QUANT_TERNARY_1_58: return launch_sk_m<QUANT_TERNARY_1_58>(p, ws, counters, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace qr

@@ -19,6 +19,14 @@ struct GemmParams {
 };
 
 hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
+
+// Small-M weight-streaming projection (M <= 64, no SwiGLU).  `ws` holds
+// skinny_workspace_floats() floats of split-K partials; `counters` one zeroed
+// uint32 per 64-column group (left zeroed on return).  Calls that share ws /
+// counters must be ordered on one stream.
+bool skinny_supported(const GemmParams& p);
+size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K, uint32_t* ksplit, uint32_t* groups);
+hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, uint32_t* counters, hipStream_t st);
 hipError_t launch_dequant(int format, const uint8_t* W, _Float16* out, uint32_t K, uint32_t N, size_t col_bytes,
                           hipStream_t st);
 

@@ -297,3 +297,40 @@ def test_prefill_layer_small(bridge, oracle):
     # Intermediates are fp16 on both sides; an fp16 tie flipped upstream can move
     # a downstream value by about one output ulp (|y| < 8 -> ulp <= 2^-8).
     assert d <= 2 * TOL
+
+
+# --------------------------------------------------------------------------
+# Small-M weight-streaming kernel (split-K across workgroups)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [1, 16, 33, 64])
+def test_skinny_split_k(bridge, oracle, fmt, M):
+    K, N = 4096, 320  # 5 column groups, K split across workgroups
+    X = synth.activations(M, K, 70 + M)
+    W = synth.quantized_weights(fmt, N, K, 71)
+    Y = empty16(M, N)
+    for _ in range(3):  # repeated calls reuse the self-resetting split-K counters
+        bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    assert maxdiff(host(Y), oracle.gemm(fmt, X, W, N)) <= TOL
+    R = synth.activations(M, N, 72)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    H, D = 5, 64
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    bridge.synchronize()
+    assert maxdiff(host(Yr), oracle.gemm(fmt, X, W, N, R=R)) <= TOL
+    assert maxdiff(host(Yh), oracle.gemm(fmt, X, W, N, head_D=D)) <= TOL
+
+
+def test_baseline_config1_full(bridge, oracle):
+    """Q4_0, M=33, K=N=4096, full output vs the oracle."""
+    M, K, N = 33, 4096, 4096
+    X = synth.activations(M, K, 10)
+    W = synth.quantized_weights(0, N, K, 11)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, 0, M, K, N)
+    bridge.synchronize()
+    assert maxdiff(host(Y), oracle.gemm(0, X, W, N)) <= TOL
