@@ -134,8 +134,9 @@ int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, 
     return 0;
 }
 
-// Split-K workspace of the small-M kernel: grow-only, counters zeroed once at
-// allocation and left zeroed by every launch.
+// Split-K workspace shared by the small-M and tiled kernels (launches are
+// ordered on the bridge stream): grow-only; counters are zeroed once at
+// allocation and every launch leaves them zeroed.
 float* g_sk_ws = nullptr;
 size_t g_sk_ws_floats = 0;
 uint32_t* g_sk_cnt = nullptr;
@@ -168,7 +169,8 @@ hipError_t ensure_skinny_ws(size_t floats, size_t groups) {
     return hipSuccess;
 }
 
-int launch(const qr::GemmParams& p) {
+int launch(const qr::GemmParams& p0) {
+    qr::GemmParams p = p0;
     if (qr::skinny_supported(p)) {
         uint32_t ks = 0, groups = 0;
         size_t floats = qr::skinny_workspace_floats(p.M, p.N, p.K, &ks, &groups);
@@ -183,6 +185,18 @@ int launch(const qr::GemmParams& p) {
             return -6;
         }
         return 0;
+    }
+    p.ksplit = qr::gemm_pick_ksplit(p);
+    if (p.ksplit > 1) {
+        uint32_t tiles = 0;
+        size_t floats = qr::gemm_workspace_floats(p, p.ksplit, &tiles);
+        hipError_t e = ensure_skinny_ws(floats, tiles);
+        if (e != hipSuccess) {
+            set_error("hipMalloc(split-K workspace)", e);
+            return -5;
+        }
+        p.ws = g_sk_ws;
+        p.counters = g_sk_cnt;
     }
     hipError_t e = qr::launch_gemm(p, g_stream);
     if (e != hipSuccess) {

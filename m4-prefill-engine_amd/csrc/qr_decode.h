@@ -1,7 +1,8 @@
 // qr_decode.h -- per-format weight decoders for gfx950.
 //
 // Each decoder turns one 32-element group of one output column into 32
-// binary16 weights, packed as 16 half2 words (word p holds elements 2p, 2p+1).
+// binary16 weights, packed as 16 half2 words (word p holds elements 2p, 2p+1);
+// decode_half(h) produces words 8h .. 8h+7 (elements 16h .. 16h+15) alone.
 // Every weight is the round-to-nearest-even binary16 of the exact value the
 // reference's double-precision CPU gold computes (tests/e2e/cpu_gold_reference.h),
 // so decoded tiles are bit-identical to the CPU unpack:
@@ -10,11 +11,13 @@
 //   Q4_K     w = q (d sc) - dmin m  cpu_gold_reference.h:121-142
 //   TERNARY  w = (c - 1) d          cpu_gold_reference.h:178-187 (code 3 -> +2d)
 // Nibble order in the 4-bit formats: byte i low nibble -> element i, high
-// nibble -> element i + 16.
+// nibble -> element i + 16, so half h of a group is the low (h = 0) or high
+// (h = 1) nibbles of all 16 code bytes.
 //
 // Loads go through a buffer resource whose base is the tile's first column,
 // so `col_off` is the byte offset of the column inside the tile.  The weight
 // base must be 4-byte aligned (the host checks and re-stages otherwise).
+// Out-of-range loads return zeros, which decode to zero weights.
 #pragma once
 #include "qr_device.h"
 #include "qr_formats.h"
@@ -34,31 +37,20 @@ template <> struct Decoder<QUANT_Q4_0> {
     static constexpr int kBlockBytes = 18;
     static constexpr int kRawWords = 5;
     __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[5]) {
-        uint32_t o = col_off + kb * 18u;
-        uint32_t a = o & ~3u;
+        const uint32_t a = (col_off + kb * 18u) & ~3u;
 #pragma unroll
         for (int i = 0; i < 5; i++) raw[i] = ld_b32(r, a + 4u * i);
     }
-    __device__ static void decode(const uint32_t raw[5], uint32_t parity2, uint32_t out[16]) {
-        uint32_t d16, q[4];
-        if (parity2) {  // block starts at byte 2 of raw[0]
-            d16 = raw[0] >> 16;
-#pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = raw[i + 1];
-        } else {
-            d16 = raw[0] & 0xffffu;
-#pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
-        }
-        h2_t d = as_h2(d16 | (d16 << 16));
+    __device__ static void decode_half(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
+        const uint32_t d16 = parity2 ? (raw[0] >> 16) : (raw[0] & 0xffffu);  // block at byte 2 of raw[0]?
+        const h2_t d = as_h2(d16 | (d16 << 16));
         const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
-            out[2 * i + 0] = as_u32((as_h2(nib_pair_lo(lo)) - off) * d);
-            out[2 * i + 1] = as_u32((as_h2(nib_pair_hi(lo)) - off) * d);
-            out[8 + 2 * i + 0] = as_u32((as_h2(nib_pair_lo(hi)) - off) * d);
-            out[8 + 2 * i + 1] = as_u32((as_h2(nib_pair_hi(hi)) - off) * d);
+            const uint32_t q = parity2 ? raw[i + 1] : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
+            const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
+            out[2 * i + 0] = as_u32((as_h2(nib_pair_lo(n)) - off) * d);
+            out[2 * i + 1] = as_u32((as_h2(nib_pair_hi(n)) - off) * d);
         }
     }
     __device__ static uint32_t parity(uint32_t col_off, uint32_t kb) { return (col_off + kb * 18u) & 2u; }
@@ -73,23 +65,20 @@ template <> struct Decoder<QUANT_MLX_4BIT> {
     static constexpr int kBlockBytes = 20;
     static constexpr int kRawWords = 5;
     __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[5]) {
-        uint32_t o = col_off + kb * 20u;
+        const uint32_t o = col_off + kb * 20u;
 #pragma unroll
         for (int i = 0; i < 5; i++) raw[i] = ld_b32(r, o + 4u * i);
     }
-    __device__ static void decode(const uint32_t raw[5], uint32_t, uint32_t out[16]) {
-        uint32_t d16 = raw[0] & 0xffffu, b16 = raw[0] >> 16;
-        h2_t d = as_h2(d16 | (d16 << 16));
-        h2_t bias = as_h2(b16 | (b16 << 16));
-        const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    __device__ static void decode_half(const uint32_t raw[5], uint32_t, int h, uint32_t out[8]) {
+        const uint32_t d16 = raw[0] & 0xffffu, b16 = raw[0] >> 16;
+        const h2_t d = as_h2(d16 | (d16 << 16));
+        const h2_t bias = as_h2(b16 | (b16 << 16));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            uint32_t q = raw[i + 1];
-            uint32_t lo = q & 0x0f0f0f0fu, hi = (q >> 4) & 0x0f0f0f0fu;
-            out[2 * i + 0] = as_u32(__builtin_elementwise_fma(as_h2(nib_pair_lo(lo)) - off, d, bias));
-            out[2 * i + 1] = as_u32(__builtin_elementwise_fma(as_h2(nib_pair_hi(lo)) - off, d, bias));
-            out[8 + 2 * i + 0] = as_u32(__builtin_elementwise_fma(as_h2(nib_pair_lo(hi)) - off, d, bias));
-            out[8 + 2 * i + 1] = as_u32(__builtin_elementwise_fma(as_h2(nib_pair_hi(hi)) - off, d, bias));
+            const uint32_t q = raw[i + 1];
+            const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
+            out[2 * i + 0] = as_u32(__builtin_elementwise_fma(magic_to_q(nib_pair_lo(n)), d, bias));
+            out[2 * i + 1] = as_u32(__builtin_elementwise_fma(magic_to_q(nib_pair_hi(n)), d, bias));
         }
     }
     __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
@@ -102,65 +91,54 @@ template <> struct Decoder<QUANT_MLX_4BIT> {
 // binade gap between d and dmin is small (e_d - e_dmin <= 3 and
 // e_dmin - e_d <= 7) the exact q*A - B has <= 24 significant bits, so one fp32
 // fma is exact and a single conversion gives the RNE binary16; otherwise the
-// exact-sum path (round-to-odd) is used.
+// exact-sum path (round-to-odd) is used, as a wave-uniform branch.
 // --------------------------------------------------------------------------
 template <> struct Decoder<QUANT_Q4_K> {
     static constexpr int kBlockElems = 32;  // decode granularity (sub-block)
     static constexpr int kBlockBytes = 144; // per 256 elements
     static constexpr int kRawWords = 8;
     __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[8]) {
-        uint32_t sb = kb >> 3, s = kb & 7u;
-        uint32_t o = col_off + sb * 144u;
-        u4_t h = ld_b128(r, o);
-        u4_t q = ld_b128(r, o + 16u + 16u * s);
-        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        const uint32_t o = col_off + (kb >> 3) * 144u;
+        const u4_t hd = ld_b128(r, o);
+        const u4_t q = ld_b128(r, o + 16u + 16u * (kb & 7u));
+        raw[0] = hd.x; raw[1] = hd.y; raw[2] = hd.z; raw[3] = hd.w;
         raw[4] = q.x; raw[5] = q.y; raw[6] = q.z; raw[7] = q.w;
     }
     __device__ static int binade(uint32_t h16) {
-        int e = (int)((h16 >> 10) & 0x1f);
+        const int e = (int)((h16 >> 10) & 0x1f);
         return (e < 1 ? 1 : e) - 15;
     }
-    __device__ static void decode(const uint32_t raw[8], uint32_t s, uint32_t out[16]) {
-        uint32_t d16 = raw[0] & 0xffffu, dm16 = raw[0] >> 16;
-        // scales[j] is byte j of raw[1..3]
-        uint64_t s03 = (uint64_t)raw[1] | ((uint64_t)raw[2] << 32);  // scales[0..7]
-        uint32_t s811 = raw[3];                                      // scales[8..11]
-        uint32_t scj = (uint32_t)(s03 >> (8u * s)) & 0xffu;
-        uint32_t sc = scj & 63u;
-        uint32_t lowm = (s < 4) ? ((s811 >> (8u * s)) & 0x0fu) : ((s811 >> (8u * (s - 4u) + 4u)) & 0x0fu);
-        uint32_t mn = lowm | ((scj >> 6) << 4);
-        float A = h2f(d16) * (float)sc;
-        float B = h2f(dm16) * (float)mn;
-        int gap = binade(d16) - binade(dm16);
-        bool fast = (A == 0.0f) || (B == 0.0f) || (gap <= 3 && gap >= -7);
+    // A, B and the exactness flag of sub-block s from the header words.
+    __device__ static void scales(const uint32_t raw[4], uint32_t s, float& A, float& B, bool& fast) {
+        const uint32_t d16 = raw[0] & 0xffffu, dm16 = raw[0] >> 16;
+        const uint64_t s07 = (uint64_t)raw[1] | ((uint64_t)raw[2] << 32);  // scales[0..7]
+        const uint32_t scj = (uint32_t)(s07 >> (8u * s)) & 0xffu;
+        const uint32_t sc = scj & 63u;
+        const uint32_t lowm = (s < 4) ? ((raw[3] >> (8u * s)) & 0x0fu) : ((raw[3] >> (8u * (s - 4u) + 4u)) & 0x0fu);
+        const uint32_t mn = lowm | ((scj >> 6) << 4);
+        A = h2f(d16) * (float)sc;
+        B = h2f(dm16) * (float)mn;
+        const int gap = binade(d16) - binade(dm16);
+        fast = (A == 0.0f) || (B == 0.0f) || (gap <= 3 && gap >= -7);
+    }
+    __device__ static void decode_half(const uint32_t raw[8], uint32_t s, int h, uint32_t out[8]) {
+        float A, B;
+        bool fast;
+        scales(raw, s, A, B, fast);
+        if (__all(fast)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t q = raw[4 + i];
-            uint32_t lo = q & 0x0f0f0f0fu, hi = (q >> 4) & 0x0f0f0f0fu;
-            uint32_t v[8];
-            if (fast) {
-                v[0] = f2h_bits(__builtin_fmaf((float)(lo & 0xffu), A, -B));
-                v[1] = f2h_bits(__builtin_fmaf((float)((lo >> 8) & 0xffu), A, -B));
-                v[2] = f2h_bits(__builtin_fmaf((float)((lo >> 16) & 0xffu), A, -B));
-                v[3] = f2h_bits(__builtin_fmaf((float)(lo >> 24), A, -B));
-                v[4] = f2h_bits(__builtin_fmaf((float)(hi & 0xffu), A, -B));
-                v[5] = f2h_bits(__builtin_fmaf((float)((hi >> 8) & 0xffu), A, -B));
-                v[6] = f2h_bits(__builtin_fmaf((float)((hi >> 16) & 0xffu), A, -B));
-                v[7] = f2h_bits(__builtin_fmaf((float)(hi >> 24), A, -B));
-            } else {
-                v[0] = rne16_sum((float)(lo & 0xffu) * A, -B);
-                v[1] = rne16_sum((float)((lo >> 8) & 0xffu) * A, -B);
-                v[2] = rne16_sum((float)((lo >> 16) & 0xffu) * A, -B);
-                v[3] = rne16_sum((float)(lo >> 24) * A, -B);
-                v[4] = rne16_sum((float)(hi & 0xffu) * A, -B);
-                v[5] = rne16_sum((float)((hi >> 8) & 0xffu) * A, -B);
-                v[6] = rne16_sum((float)((hi >> 16) & 0xffu) * A, -B);
-                v[7] = rne16_sum((float)(hi >> 24) * A, -B);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t n = (h ? (raw[4 + i] >> 4) : raw[4 + i]) & 0x0f0f0f0fu;
+                out[2 * i + 0] = affine_pair_exact(nib_pair_lo(n), A, -B);
+                out[2 * i + 1] = affine_pair_exact(nib_pair_hi(n), A, -B);
             }
-            out[2 * i + 0] = pack_h2(v[0], v[1]);
-            out[2 * i + 1] = pack_h2(v[2], v[3]);
-            out[8 + 2 * i + 0] = pack_h2(v[4], v[5]);
-            out[8 + 2 * i + 1] = pack_h2(v[6], v[7]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t n = (h ? (raw[4 + i] >> 4) : raw[4 + i]) & 0x0f0f0f0fu;
+                out[2 * i + 0] = affine_pair_any(nib_pair_lo(n), A, -B, fast);
+                out[2 * i + 1] = affine_pair_any(nib_pair_hi(n), A, -B, fast);
+            }
         }
     }
     __device__ static uint32_t parity(uint32_t, uint32_t kb) { return kb & 7u; }
@@ -176,33 +154,37 @@ template <> struct Decoder<QUANT_TERNARY_1_58> {
     static constexpr int kBlockBytes = 12;
     static constexpr int kRawWords = 3;
     __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[3]) {
-        uint32_t o = col_off + kb * 12u;
+        const uint32_t o = col_off + kb * 12u;
 #pragma unroll
         for (int i = 0; i < 3; i++) raw[i] = ld_b32(r, o + 4u * i);
     }
-    __device__ static void decode(const uint32_t raw[3], uint32_t, uint32_t out[16]) {
-        uint32_t d16 = raw[0] & 0xffffu;
-        h2_t d = as_h2(d16 | (d16 << 16));
+    __device__ static void decode_half(const uint32_t raw[3], uint32_t, int h, uint32_t out[8]) {
+        const uint32_t d16 = raw[0] & 0xffffu;
+        const h2_t d = as_h2(d16 | (d16 << 16));
         const h2_t off = {(_Float16)1025.0f, (_Float16)1025.0f};
+        const uint32_t q = h ? raw[2] : raw[1];
+        const uint32_t ev = q & 0x33333333u;         // codes of even elements, one per nibble
+        const uint32_t od = (q >> 2) & 0x33333333u;  // codes of odd elements
+        const uint32_t ev_lo = ev & 0x0f0f0f0fu, ev_hi = (ev >> 4) & 0x0f0f0f0fu;
+        const uint32_t od_lo = od & 0x0f0f0f0fu, od_hi = (od >> 4) & 0x0f0f0f0fu;
+        // nibble j (elements 2j, 2j+1): j even -> byte j/2 of *_lo, j odd -> of *_hi
 #pragma unroll
-        for (int w = 0; w < 2; w++) {
-            uint32_t q = raw[1 + w];
-            uint32_t ev = q & 0x33333333u;         // codes of even elements, one per nibble
-            uint32_t od = (q >> 2) & 0x33333333u;  // codes of odd elements
-            uint32_t ev_lo = ev & 0x0f0f0f0fu, ev_hi = (ev >> 4) & 0x0f0f0f0fu;
-            uint32_t od_lo = od & 0x0f0f0f0fu, od_hi = (od >> 4) & 0x0f0f0f0fu;
-            // nibble j (elements 2j, 2j+1): j even -> byte j/2 of *_lo, j odd -> of *_hi
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)(b + 4) << 16);
-                uint32_t p0 = perm(od_lo, ev_lo, sel) | 0x64006400u;  // nibble 2b
-                uint32_t p1 = perm(od_hi, ev_hi, sel) | 0x64006400u;  // nibble 2b+1
-                out[8 * w + 2 * b + 0] = as_u32((as_h2(p0) - off) * d);
-                out[8 * w + 2 * b + 1] = as_u32((as_h2(p1) - off) * d);
-            }
+        for (int b = 0; b < 4; b++) {
+            const uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)(b + 4) << 16);
+            const uint32_t p0 = perm(od_lo, ev_lo, sel) | 0x64006400u;  // nibble 2b
+            const uint32_t p1 = perm(od_hi, ev_hi, sel) | 0x64006400u;  // nibble 2b+1
+            out[2 * b + 0] = as_u32((as_h2(p0) - off) * d);
+            out[2 * b + 1] = as_u32((as_h2(p1) - off) * d);
         }
     }
     __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
 };
+
+// Whole group: words 0..15.
+template <int F>
+__device__ __forceinline__ void decode_group(const uint32_t* raw, uint32_t parity, uint32_t out[16]) {
+    Decoder<F>::decode_half(raw, parity, 0, out);
+    Decoder<F>::decode_half(raw, parity, 1, out + 8);
+}
 
 }  // namespace qr

@@ -70,4 +70,29 @@ __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel)
 __device__ __forceinline__ uint32_t nib_pair_lo(uint32_t x) { return perm(0x64646464u, x, 0x04010400u); }
 __device__ __forceinline__ uint32_t nib_pair_hi(uint32_t x) { return perm(0x64646464u, x, 0x04030402u); }
 
+// {q0, q1} from a magic pair {1024 + q0, 1024 + q1}: exact halves.
+__device__ __forceinline__ h2_t magic_to_q(uint32_t magic_pair) {
+    const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    return as_h2(magic_pair) - off;
+}
+
+// RNE binary16 of q*A + C for both codes of a magic pair, when q*A + C is
+// exact in fp32 (fused fp32 fma of the fp16 code, one rounding to fp16; maps
+// to v_fma_mix{lo,hi}_f16).
+__device__ __forceinline__ uint32_t affine_pair_exact(uint32_t magic_pair, float A, float C) {
+    const h2_t q = magic_to_q(magic_pair);
+    const _Float16 lo = (_Float16)__builtin_fmaf((float)q.x, A, C);
+    const _Float16 hi = (_Float16)__builtin_fmaf((float)q.y, A, C);
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+// Same for any inputs: the exact-sum (round-to-odd) path where `exact` is false.
+__device__ __forceinline__ uint32_t affine_pair_any(uint32_t magic_pair, float A, float C, bool exact) {
+    const h2_t q = magic_to_q(magic_pair);
+    const float q0 = (float)q.x, q1 = (float)q.y;
+    const uint32_t lo = exact ? f2h_bits(__builtin_fmaf(q0, A, C)) : rne16_sum(q0 * A, C);
+    const uint32_t hi = exact ? f2h_bits(__builtin_fmaf(q1, A, C)) : rne16_sum(q1 * A, C);
+    return lo | (hi << 16);
+}
+
 }  // namespace qr

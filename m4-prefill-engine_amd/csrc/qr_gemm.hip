@@ -1,23 +1,33 @@
-// qr_gemm.hip -- quantized projection Y = X . W^T on gfx950 MFMA.
+// qr_gemm.hip -- quantized projection Y = X . W^T on gfx950 MFMA (tiled, M > 64).
 //
 // Replaces the reference's block_mma_64x64_engine (quant_router_kernels.metal:
 // 442-581) and its 14 entry points (:588-927), and the fused dual-projection
 // SwiGLU swiglu_mma_dual_simd (brick3_swiglu_kernels.metal:428-698).
 //
-// Design (one workgroup = 4 wave64s, one BM x BN output tile):
+// Design (one workgroup = 4 or 8 wave64s, one BM x BN output tile, the K range
+// split across `ksplit` workgroups when the tile grid alone cannot fill the GPU):
 //  * K advances 64 per step (two 32-element weight groups per column).
-//  * X tile [BM x 64] fp16 is loaded with 16-byte buffer loads; the weight
-//    groups of the BN columns are loaded raw (compressed) and decoded in
-//    registers to binary16 (qr_decode.h, bit-exact vs the CPU unpack), then
-//    both are written to a double-buffered LDS stage.  Loads for step k+1 are
-//    issued before the MFMAs of step k, so the HBM latency hides under MFMA.
-//  * Each wave computes a (TM*32) x (TN*32) sub-tile with
-//    v_mfma_f32_32x32x16_f16 (fp32 accumulation).  Both operands are
-//    K-contiguous in LDS, so every lane fetches its 8 halfs with one
-//    ds_read_b128; rows are padded by 8 halfs to spread LDS banks.
-//  * Epilogue: fp32 accumulator (+ optional fp16 residual, + SwiGLU for the
-//    dual variant) rounded once to fp16, written [M, N] or head-major
-//    [H, M, D] (direct-head routing, quant_router_kernels.metal:570-574).
+//  * The X tile [BM x 64] fp16 is fetched with 16-byte buffer loads; the
+//    weight groups of the BN columns are fetched raw (compressed) and decoded
+//    in registers to binary16 (qr_decode.h, bit-exact vs the CPU unpack), a
+//    half group (16 elements) per thread when the workgroup has enough threads.
+//    Fetches run P steps ahead of the MFMAs (P register stages), so HBM/L2
+//    latency hides behind P-1 steps of matrix work.
+//  * Decoded tiles go to a double-buffered LDS stage (one barrier per step).
+//    Both operands are K-contiguous, so each lane fetches its 8 halfs of a
+//    v_mfma_f32_32x32x16_f16 operand with one ds_read_b128; rows are padded
+//    by 8 halfs to spread the LDS banks.  With 8 waves, two waves share each
+//    SIMD, so one wave's decode VALU work overlaps the other's MFMAs.
+//  * Tiles are assigned XCD-aware: consecutive workgroup ids land on
+//    different XCDs, so ids are remapped to give each XCD a contiguous run of
+//    tiles grouped 2 row-tiles x many column-tiles (shared L2 reuse of X
+//    rows and weight columns).
+//  * Epilogue: fp32 accumulators (+ fp16 residual, + SwiGLU for the dual
+//    variant) rounded once to fp16, written [M, N] or head-major [H, M, D]
+//    (quant_router_kernels.metal:570-574).  With a K split, the partial
+//    accumulators go to a workspace with agent-scope stores and the last
+//    workgroup of the tile (agent-scope counter) sums them in split order --
+//    deterministic, one launch.
 #include "qr_decode.h"
 #include "qr_kernels.h"
 
@@ -28,24 +38,45 @@ constexpr int kLdsRow = kBK + 8;  // halfs per LDS row (padding vs bank conflict
 
 template <int F, int WGM, int WGN, int TM, int TN, bool DUAL>
 struct GemmCfg {
+    static constexpr int NT = 64 * WGM * WGN;             // threads
     static constexpr int BM = WGM * TM * 32;
     static constexpr int BN = WGN * TN * 32;
     static constexpr int NCOL = DUAL ? 2 * BN : BN;       // weight columns decoded per step
-    static constexpr int UNITS = NCOL * 2;                // 32-element groups per step
-    static constexpr int UPT = (UNITS + 255) / 256;       // groups per thread
+    static constexpr int HALVES = NCOL * 4;               // 16-element half groups per step
+    static constexpr bool HALF = NT >= HALVES;            // one half group per thread
+    static constexpr int UNITS = HALF ? HALVES : NCOL * 2;
+    static constexpr int UPT = (UNITS + NT - 1) / NT;     // decode units per thread
     static constexpr int XCH = BM * kBK / 8;              // 16-byte X chunks per step
-    static constexpr int XPT = (XCH + 255) / 256;
+    static constexpr int XPT = (XCH + NT - 1) / NT;
     static constexpr int LDS_A = BM * kLdsRow;            // halfs per stage
     static constexpr int LDS_B = NCOL * kLdsRow;
     static constexpr int LDS_STAGE = LDS_A + LDS_B;
-    static_assert(WGM * WGN == 4, "4 waves per workgroup");
+    static constexpr int ACC = TM * TN * 16 * (DUAL ? 2 : 1);  // accumulator floats per lane
+    static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves per workgroup");
 };
 
-template <int F, int WGM, int WGN, int TM, int TN, bool DUAL>
-__global__ void __launch_bounds__(256)
+// Tile of workgroup `bid` among T tiles (nt_m x nt_n): XCD-contiguous runs,
+// grouped two row-tiles at a time.
+__device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t& tm, uint32_t& tn) {
+    const uint32_t T = nt_m * nt_n;
+    uint32_t t = bid;
+    if (T % 8 == 0) t = (bid % 8) * (T / 8) + bid / 8;
+    constexpr uint32_t GM = 2;
+    const uint32_t per_group = GM * nt_n;
+    const uint32_t grp = t / per_group;
+    const uint32_t first = grp * GM;
+    const uint32_t gm = min(GM, nt_m - first);
+    const uint32_t in = t % per_group;
+    tm = first + in % gm;
+    tn = in / gm;
+}
+
+template <int F, int WGM, int WGN, int TM, int TN, bool DUAL, int P>
+__global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_kernel(GemmParams p) {
     using C = GemmCfg<F, WGM, WGN, TM, TN, DUAL>;
     using Dec = Decoder<F>;
+    constexpr int NT = C::NT;
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
 
     const int tid = threadIdx.x;
@@ -53,81 +84,100 @@ gemm_kernel(GemmParams p) {
     const int wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
 
-    // Grid: x = N tiles, y = M tiles.
-    const int n0 = blockIdx.x * C::BN;
-    const int m0 = blockIdx.y * C::BM;
-    const uint32_t K = p.K;
-    const uint32_t nsteps = (K + kBK - 1) / kBK;
-    const uint32_t ngroups = K / 32;                       // 32-element groups per column
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t nt_m = (M + C::BM - 1) / C::BM, nt_n = (N + C::BN - 1) / C::BN;
+    uint32_t tmi, tni;
+    tile_of(blockIdx.x, nt_m, nt_n, tmi, tni);
+    const int m0 = tmi * C::BM, n0 = tni * C::BN;
+    const uint32_t ksplit = p.ksplit ? p.ksplit : 1;
+    const uint32_t kz = blockIdx.y;
+    const uint32_t Kc = K / ksplit;                        // host guarantees divisibility
+    const uint32_t k_begin = kz * Kc;
+    const uint32_t nsteps = (Kc + kBK - 1) / kBK;
+    const uint32_t g_begin = k_begin / 32, g_end = (k_begin + Kc) / 32;
     const uint32_t col_bytes = (uint32_t)p.col_bytes;
 
-    // Buffer resources: X rows of this tile; W columns of this tile.
-    const int mrows = min(C::BM, (int)p.M - m0);
-    const int ncols = min(C::BN, (int)p.N - n0);
+    const int mrows = min(C::BM, (int)M - m0);
+    const int ncols = min(C::BN, (int)N - n0);
     auto xr = make_rsrc(p.X + (size_t)m0 * K, (uint32_t)mrows * K * 2u);
     auto wr0 = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
     auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
 
-    uint32_t xraw[C::XPT][4];
-    uint32_t wraw[C::UPT][Dec::kRawWords];
+    uint32_t xraw[P][C::XPT][4];
+    uint32_t wraw[P][C::UPT][Dec::kRawWords];
 
-    auto load_step = [&](uint32_t step) {
-        const uint32_t k0 = step * kBK;
-#pragma unroll
-        for (int i = 0; i < C::XPT; i++) {
-            int c = tid + 256 * i;
-            int row = c >> 3, kc = c & 7;
-            uint32_t k = k0 + kc * 8;
-            uint32_t off = (c < C::XCH && k < K) ? ((uint32_t)row * K + k) * 2u : kOOB;
-            u4_t v = ld_b128(xr, off);
-            xraw[i][0] = v.x; xraw[i][1] = v.y; xraw[i][2] = v.z; xraw[i][3] = v.w;
-        }
-#pragma unroll
-        for (int u = 0; u < C::UPT; u++) {
-            int unit = tid + 256 * u;
-            int col = unit >> 1;
-            uint32_t g = step * 2 + (unit & 1);
-            bool dual_up = DUAL && col >= C::BN;
-            int lcol = dual_up ? col - C::BN : col;
-            uint32_t coff = (unit < C::UNITS && g < ngroups && lcol < ncols) ? (uint32_t)lcol * col_bytes : kOOB;
-            if (coff == kOOB) {
-#pragma unroll
-                for (int j = 0; j < Dec::kRawWords; j++) wraw[u][j] = 0;
-            } else {
-                Dec::load(dual_up ? wr1 : wr0, coff, g, wraw[u]);
-            }
+    // decode unit u of this thread: weight column, group within the step, half
+    auto unit_of = [&](int u, int& col, int& gsel, int& half) {
+        const int unit = tid + NT * u;
+        if (C::HALF) {
+            col = unit >> 2;
+            gsel = (unit >> 1) & 1;
+            half = unit & 1;
+        } else {
+            col = unit >> 1;
+            gsel = unit & 1;
+            half = -1;
         }
     };
 
-    auto store_step = [&](uint32_t step, int stage) {
+    auto load_step = [&](uint32_t step, int slot) {
+        const uint32_t k0 = k_begin + step * kBK;
+#pragma unroll
+        for (int i = 0; i < C::XPT; i++) {
+            const int c = tid + NT * i;
+            const int row = c >> 3, kc = c & 7;
+            const uint32_t k = k0 + kc * 8;
+            const uint32_t off = (c < C::XCH && k < k_begin + Kc) ? ((uint32_t)row * K + k) * 2u : kOOB;
+            const u4_t v = ld_b128(xr, off);
+            xraw[slot][i][0] = v.x; xraw[slot][i][1] = v.y; xraw[slot][i][2] = v.z; xraw[slot][i][3] = v.w;
+        }
+#pragma unroll
+        for (int u = 0; u < C::UPT; u++) {
+            int col, gsel, half;
+            unit_of(u, col, gsel, half);
+            const uint32_t g = g_begin + step * 2 + gsel;
+            const bool up = DUAL && col >= C::BN;
+            const int lcol = up ? col - C::BN : col;
+            // out-of-range groups read as zeros (buffer bounds) and decode to zeros
+            const uint32_t coff = (tid + NT * u < C::UNITS && g < g_end) ? (uint32_t)lcol * col_bytes : kOOB;
+            Dec::load(up ? wr1 : wr0, coff, coff == kOOB ? 0u : g, wraw[slot][u]);
+        }
+    };
+
+    auto store_step = [&](uint32_t step, int slot, int stage) {
         _Float16* As = lds + stage * C::LDS_STAGE;
         _Float16* Bs = As + C::LDS_A;
 #pragma unroll
         for (int i = 0; i < C::XPT; i++) {
-            int c = tid + 256 * i;
+            const int c = tid + NT * i;
             if (c < C::XCH) {
-                int row = c >> 3, kc = c & 7;
-                u4_t v = {xraw[i][0], xraw[i][1], xraw[i][2], xraw[i][3]};
-                *reinterpret_cast<u4_t*>(As + row * kLdsRow + kc * 8) = v;
+                const int row = c >> 3, kc = c & 7;
+                *reinterpret_cast<u4_t*>(As + row * kLdsRow + kc * 8) =
+                    u4_t{xraw[slot][i][0], xraw[slot][i][1], xraw[slot][i][2], xraw[slot][i][3]};
             }
         }
 #pragma unroll
         for (int u = 0; u < C::UPT; u++) {
-            int unit = tid + 256 * u;
-            if (unit < C::UNITS) {
-                int col = unit >> 1;
-                uint32_t g = step * 2 + (unit & 1);
-                int lcol = (DUAL && col >= C::BN) ? col - C::BN : col;
-                uint32_t out[16];
-                if (g < ngroups && lcol < ncols) {
-                    Dec::decode(wraw[u], Dec::parity((uint32_t)lcol * col_bytes, g), out);
+            if (tid + NT * u < C::UNITS) {
+                int col, gsel, half;
+                unit_of(u, col, gsel, half);
+                const uint32_t g = g_begin + step * 2 + gsel;
+                const int lcol = (DUAL && col >= C::BN) ? col - C::BN : col;
+                const uint32_t par = Dec::parity((uint32_t)lcol * col_bytes, g);
+                if (C::HALF) {
+                    uint32_t out[8];
+                    Dec::decode_half(wraw[slot][u], par, half, out);
+                    u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + gsel * 32 + half * 16);
+                    dst[0] = u4_t{out[0], out[1], out[2], out[3]};
+                    dst[1] = u4_t{out[4], out[5], out[6], out[7]};
                 } else {
+                    uint32_t out[16];
+                    decode_group<F>(wraw[slot][u], par, out);
+                    u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + gsel * 32);
 #pragma unroll
-                    for (int j = 0; j < 16; j++) out[j] = 0;
+                    for (int j = 0; j < 4; j++)
+                        dst[j] = u4_t{out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]};
                 }
-                u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + (unit & 1) * 32);
-#pragma unroll
-                for (int j = 0; j < 4; j++) dst[j] = u4_t{out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]};
             }
         }
     };
@@ -145,17 +195,11 @@ gemm_kernel(GemmParams p) {
             for (int j = 0; j < TN; j++) acc2[i][j] = f16v_t{};
     }
 
-    load_step(0);
-    store_step(0, 0);
-    __syncthreads();
-
     const int arow = wm * TM * 32 + (lane & 31);
     const int bcol = wn * TN * 32 + (lane & 31);
     const int kq = (lane >> 5) * 8;
 
-    for (uint32_t s = 0; s < nsteps; s++) {
-        const int stage = s & 1;
-        if (s + 1 < nsteps) load_step(s + 1);
+    auto compute = [&](int stage) {
         const _Float16* As = lds + stage * C::LDS_STAGE;
         const _Float16* Bs = As + C::LDS_A;
 #pragma unroll
@@ -184,13 +228,88 @@ gemm_kernel(GemmParams p) {
                         acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b2[j], acc2[i][j], 0, 0, 0);
             }
         }
-        if (s + 1 < nsteps) store_step(s + 1, stage ^ 1);
-        __syncthreads();
+    };
+
+    // ---- prologue: fill the P register stages, stage step 0 into LDS ----
+#pragma unroll
+    for (int j = 0; j < P; j++)
+        if ((uint32_t)j < nsteps) load_step(j, j);
+    store_step(0, 0, 0);
+    if ((uint32_t)P < nsteps) load_step(P, 0);
+    __syncthreads();
+
+    // ---- main loop, unrolled by P so register stages are static ----
+    for (uint32_t s0 = 0; s0 < nsteps; s0 += P) {
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            const uint32_t s = s0 + j;
+            if (s < nsteps) {
+                compute(s & 1);
+                if (s + 1 < nsteps) {
+                    const int slot = (j + 1) % P;
+                    store_step(s + 1, slot, (s + 1) & 1);
+                    if (s + 1 + P < nsteps) load_step(s + 1 + P, slot);
+                }
+                __syncthreads();
+            }
+        }
     }
 
-    // Epilogue.  Accumulator element r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
-    // column l%32 of the 32x32 MFMA tile.
-    const uint32_t M = p.M, N = p.N;
+    // ---- split-K: publish partials, the last workgroup of the tile sums ----
+    if (ksplit > 1) {
+        const uint32_t T = nt_m * nt_n;
+        const uint32_t tile = tmi * nt_n + tni;
+        float* slot = p.ws + ((size_t)kz * T + tile) * (C::ACC * NT) + tid;
+        int e = 0;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++, e++) {
+                    __hip_atomic_store(slot + e * NT, acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if constexpr (DUAL)
+                        __hip_atomic_store(slot + (C::ACC / 2 + e) * NT, acc2[i][j][r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
+        __syncthreads();
+        __shared__ uint32_t s_last;
+        if (tid == 0) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = (prev == ksplit - 1) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        // sum all splits in split order (deterministic)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                acc[i][j] = f16v_t{};
+                if constexpr (DUAL) acc2[i][j] = f16v_t{};
+            }
+        for (uint32_t z = 0; z < ksplit; z++) {
+            const float* src = p.ws + ((size_t)z * T + tile) * (C::ACC * NT) + tid;
+            int e2 = 0;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++, e2++) {
+                        acc[i][j][r] += __hip_atomic_load(src + e2 * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if constexpr (DUAL)
+                            acc2[i][j][r] += __hip_atomic_load(src + (C::ACC / 2 + e2) * NT, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
+                    }
+        }
+        if (tid == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- epilogue: accumulator element r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
+    // column l%32 of the 32x32 MFMA tile ----
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -202,13 +321,13 @@ gemm_kernel(GemmParams p) {
                 if (m < (int)M && n < (int)N) {
                     float v = acc[i][j][r];
                     if constexpr (DUAL) {
-                        float u = acc2[i][j][r];
+                        const float u = acc2[i][j][r];
                         v = v / (1.0f + __expf(-v)) * u;
                     }
                     if (p.R) v += (float)p.R[(size_t)m * N + n];
                     size_t o;
                     if (p.head_D) {
-                        uint32_t h = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
+                        const uint32_t h = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
                         o = ((size_t)h * M + m) * p.head_D + dd;
                     } else {
                         o = (size_t)m * N + n;
@@ -219,10 +338,36 @@ gemm_kernel(GemmParams p) {
         }
 }
 
+#ifndef QR_GEMM_STAGES
+#define QR_GEMM_STAGES 3
+#endif
+
+// Tile configurations: {waves_m, waves_n, tiles_m, tiles_n} -> BM x BN.
+//   0: 8 waves 4x2, 2x2 tiles -> 256 x 128  (large M)
+//   1: 4 waves 2x2, 2x2 tiles -> 128 x 128  (medium M)
+//   2: 4 waves 2x2, 1x2 tiles ->  64 x 128
+//   dual (SwiGLU): 3: 8 waves 4x2, 1x1 -> 128 x 64 ; 4: 4 waves 2x2, 1x1 -> 64 x 64
+static int pick_shape(uint32_t M, bool dual) {
+    if (dual) return M > 64 ? 3 : 4;
+    if (M >= 1024) return 0;
+    if (M > 64) return 1;
+    return 2;
+}
+
+static void shape_dims(int shape, uint32_t& bm, uint32_t& bn) {
+    switch (shape) {
+        case 0: bm = 256; bn = 128; return;
+        case 1: bm = 128; bn = 128; return;
+        case 2: bm = 64; bn = 128; return;
+        case 3: bm = 128; bn = 64; return;
+        default: bm = 64; bn = 64; return;
+    }
+}
+
 template <int F, int WGM, int WGN, int TM, int TN, bool DUAL>
 static hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
     using C = GemmCfg<F, WGM, WGN, TM, TN, DUAL>;
-    auto kern = gemm_kernel<F, WGM, WGN, TM, TN, DUAL>;
+    auto kern = gemm_kernel<F, WGM, WGN, TM, TN, DUAL, QR_GEMM_STAGES>;
     const size_t lds = 2 * C::LDS_STAGE * sizeof(_Float16);
     static bool attr_set = false;  // per instantiation
     if (!attr_set) {
@@ -230,21 +375,46 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    dim3 grid((p.N + C::BN - 1) / C::BN, (p.M + C::BM - 1) / C::BM);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, p);
+    const uint32_t T = ((p.M + C::BM - 1) / C::BM) * ((p.N + C::BN - 1) / C::BN);
+    const uint32_t ks = p.ksplit ? p.ksplit : 1;
+    hipLaunchKernelGGL(kern, dim3(T, ks), dim3(C::NT), lds, st, p);
     return hipGetLastError();
+}
+
+uint32_t gemm_pick_ksplit(const GemmParams& p) {
+    const bool dual = p.W2 != nullptr;
+    if (dual) return 1;
+    uint32_t bm, bn;
+    shape_dims(pick_shape(p.M, dual), bm, bn);
+    const uint32_t T = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+    uint32_t ks = 1;
+    // split K until the grid covers the 256 CUs; each split keeps >= 1024 of K
+    // and a whole number of 256-element super-blocks
+    while (T * ks < 256 && p.K % (256 * ks * 2) == 0 && p.K / (ks * 2) >= 1024) ks *= 2;
+    return ks;
+}
+
+size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
+    uint32_t bm, bn;
+    const bool dual = p.W2 != nullptr;
+    shape_dims(pick_shape(p.M, dual), bm, bn);
+    const uint32_t T = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+    if (tiles) *tiles = T;
+    return ks > 1 ? (size_t)ks * T * bm * bn * (dual ? 2 : 1) : 0;
 }
 
 template <int F, bool DUAL>
 static hipError_t launch_fmt(const GemmParams& p, hipStream_t st) {
-    if (DUAL) {
-        if (p.M <= 32) return launch_cfg<F, 1, 4, 1, 1, DUAL>(p, st);
-        return launch_cfg<F, 2, 2, 2, 1, DUAL>(p, st);
+    if constexpr (DUAL) {
+        if (pick_shape(p.M, true) == 3) return launch_cfg<F, 4, 2, 1, 1, true>(p, st);
+        return launch_cfg<F, 2, 2, 1, 1, true>(p, st);
+    } else {
+        switch (pick_shape(p.M, false)) {
+            case 0: return launch_cfg<F, 4, 2, 2, 2, false>(p, st);
+            case 1: return launch_cfg<F, 2, 2, 2, 2, false>(p, st);
+            default: return launch_cfg<F, 2, 2, 1, 2, false>(p, st);
+        }
     }
-    if (p.M <= 32) return launch_cfg<F, 1, 4, 1, 1, DUAL>(p, st);
-    if (p.M <= 64) return launch_cfg<F, 2, 2, 1, 1, DUAL>(p, st);
-    if (p.M <= 512) return launch_cfg<F, 2, 2, 2, 2, DUAL>(p, st);
-    return launch_cfg<F, 2, 2, 4, 2, DUAL>(p, st);
 }
 
 hipError_t launch_gemm(const GemmParams& p, hipStream_t st) {
@@ -256,44 +426,6 @@ hipError_t launch_gemm(const GemmParams& p, hipStream_t st) {
         case QUANT_TERNARY_1_58: return dual ? launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
         default: return hipErrorInvalidValue;
     }
-}
-
-// --------------------------------------------------------------------------
-// Dequantize [N, K] weights to binary16 with the same decoders the GEMM uses
-// (bit-exact contract check; also the reference registry's dequantize hook,
-// src/router/quant_registry.h:24).  One thread per 32-element group.
-// --------------------------------------------------------------------------
-template <int F>
-__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* W, _Float16* out, uint32_t K, uint32_t N,
-                                                      uint32_t col_bytes) {
-    using Dec = Decoder<F>;
-    const uint32_t ng = K / 32;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)ng * N) return;
-    const uint32_t n = (uint32_t)(idx / ng), g = (uint32_t)(idx % ng);
-    // Base at the (4-byte aligned) start of W; the column offset carries the
-    // 2-byte parity of 18-byte Q4_0 columns.
-    auto r = make_rsrc(W, (uint32_t)((size_t)col_bytes * N));
-    uint32_t raw[Dec::kRawWords], o[16];
-    Dec::load(r, n * col_bytes, g, raw);
-    Dec::decode(raw, Dec::parity(n * col_bytes, g), o);
-    u4_t* dst = reinterpret_cast<u4_t*>(out + (size_t)n * K + (size_t)g * 32);
-#pragma unroll
-    for (int j = 0; j < 4; j++) dst[j] = u4_t{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
-}
-
-hipError_t launch_dequant(int format, const uint8_t* W, _Float16* out, uint32_t K, uint32_t N, size_t col_bytes,
-                          hipStream_t st) {
-    const size_t total = (size_t)(K / 32) * N;
-    dim3 grid((unsigned)((total + 255) / 256));
-    switch (format) {
-        case QUANT_Q4_0: hipLaunchKernelGGL(dequant_kernel<QUANT_Q4_0>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
-        case QUANT_MLX_4BIT: hipLaunchKernelGGL(dequant_kernel<QUANT_MLX_4BIT>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
-        case QUANT_Q4_K: hipLaunchKernelGGL(dequant_kernel<QUANT_Q4_K>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
-        case QUANT_TERNARY_1_58: hipLaunchKernelGGL(dequant_kernel<QUANT_TERNARY_1_58>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
 }
 
 }  // namespace qr

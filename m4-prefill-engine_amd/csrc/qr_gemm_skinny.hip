@@ -131,14 +131,14 @@ template <> struct Frag<QUANT_Q4_K> {
         if (g >= 2) { q0 >>= 4; q1 >>= 4; }
         q0 &= 0x0f0f0f0fu;
         q1 &= 0x0f0f0f0fu;
-        uint32_t v[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float c0 = (float)((q0 >> (8 * i)) & 0xffu), c1 = (float)((q1 >> (8 * i)) & 0xffu);
-            v[i] = fast ? f2h_bits(__builtin_fmaf(c0, A, -B)) : rne16_sum(c0 * A, -B);
-            v[4 + i] = fast ? f2h_bits(__builtin_fmaf(c1, A, -B)) : rne16_sum(c1 * A, -B);
+        u4_t w;
+        if (__all(fast)) {  // exact-sum path only when some lane needs it
+            w = u4_t{affine_pair_exact(nib_pair_lo(q0), A, -B), affine_pair_exact(nib_pair_hi(q0), A, -B),
+                     affine_pair_exact(nib_pair_lo(q1), A, -B), affine_pair_exact(nib_pair_hi(q1), A, -B)};
+        } else {
+            w = u4_t{affine_pair_any(nib_pair_lo(q0), A, -B, fast), affine_pair_any(nib_pair_hi(q0), A, -B, fast),
+                     affine_pair_any(nib_pair_lo(q1), A, -B, fast), affine_pair_any(nib_pair_hi(q1), A, -B, fast)};
         }
-        u4_t w = {pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7])};
         return __builtin_bit_cast(h8_t, w);
     }
 };

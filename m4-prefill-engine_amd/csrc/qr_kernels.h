@@ -16,9 +16,17 @@ struct GemmParams {
     uint32_t M, N, K;
     uint32_t head_D;      // 0: Y is [M, N]; else direct-head [N / head_D, M, head_D]
     size_t col_bytes;     // bytes of one weight column
+    // K split across workgroups (tiled kernel): 0/1 = none.  `ws` holds
+    // gemm_workspace_floats() floats, `counters` one zeroed uint32 per tile
+    // (left zeroed on return).
+    uint32_t ksplit;
+    float* ws;
+    uint32_t* counters;
 };
 
 hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
+uint32_t gemm_pick_ksplit(const GemmParams& p);
+size_t gemm_workspace_floats(const GemmParams& p, uint32_t ksplit, uint32_t* tiles);
 
 // Small-M weight-streaming projection (M <= 64, no SwiGLU).  `ws` holds
 // skinny_workspace_floats() floats of split-K partials; `counters` one zeroed

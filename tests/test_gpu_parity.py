@@ -334,3 +334,21 @@ def test_baseline_config1_full(bridge, oracle):
     bridge.dispatch_gemm(dev(X), dev(W), Y, 0, M, K, N)
     bridge.synchronize()
     assert maxdiff(host(Y), oracle.gemm(0, X, W, N)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [65, 129, 300])
+def test_tiled_split_k(bridge, oracle, fmt, M):
+    """Tiled kernel with the K range split across workgroups (few tiles)."""
+    K, N = 4096, 384
+    X = synth.activations(M, K, 80 + M)
+    W = synth.quantized_weights(fmt, N, K, 81)
+    Y = empty16(M, N)
+    for _ in range(2):
+        bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    R = synth.activations(M, N, 82)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    bridge.synchronize()
+    assert maxdiff(host(Y), oracle.gemm(fmt, X, W, N)) <= TOL
+    assert maxdiff(host(Yr), oracle.gemm(fmt, X, W, N, R=R)) <= TOL
