@@ -166,7 +166,12 @@ gemm_kernel(GemmParams p) {
                 const uint32_t par = Dec::parity((uint32_t)lcol * col_bytes, g);
                 if (C::HALF) {
                     uint32_t out[8];
+#ifdef QR_GEMM_NODECODE  // timing experiment only: raw words instead of decoded weights
+#pragma unroll
+                    for (int q = 0; q < 8; q++) out[q] = wraw[slot][u][q % Dec::kRawWords] ^ par;
+#else
                     Dec::decode_half(wraw[slot][u], par, half, out);
+#endif
                     u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + gsel * 32 + half * 16);
                     dst[0] = u4_t{out[0], out[1], out[2], out[3]};
                     dst[1] = u4_t{out[4], out[5], out[6], out[7]};
@@ -346,7 +351,8 @@ gemm_kernel(GemmParams p) {
 //   0: 8 waves 4x2, 2x2 tiles -> 256 x 128  (large M)
 //   1: 4 waves 2x2, 2x2 tiles -> 128 x 128  (medium M)
 //   2: 4 waves 2x2, 1x2 tiles ->  64 x 128
-//   dual (SwiGLU): 3: 8 waves 4x2, 1x1 -> 128 x 64 ; 4: 4 waves 2x2, 1x1 -> 64 x 64
+//   dual (SwiGLU): 3: 8 waves 4x2, 2x1 -> 256 x 64 (gate + up: 128 weight
+//   columns per step); 4: 4 waves 2x2, 1x1 -> 64 x 64
 static int pick_shape(uint32_t M, bool dual) {
     if (dual) return M > 64 ? 3 : 4;
     if (M >= 1024) return 0;
@@ -359,7 +365,7 @@ static void shape_dims(int shape, uint32_t& bm, uint32_t& bn) {
         case 0: bm = 256; bn = 128; return;
         case 1: bm = 128; bn = 128; return;
         case 2: bm = 64; bn = 128; return;
-        case 3: bm = 128; bn = 64; return;
+        case 3: bm = 256; bn = 64; return;
         default: bm = 64; bn = 64; return;
     }
 }
@@ -406,7 +412,15 @@ size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) 
 template <int F, bool DUAL>
 static hipError_t launch_fmt(const GemmParams& p, hipStream_t st) {
     if constexpr (DUAL) {
-        if (pick_shape(p.M, true) == 3) return launch_cfg<F, 4, 2, 1, 1, true>(p, st);
+#ifndef QR_DUAL_CFG
+#define QR_DUAL_CFG 2
+#endif
+        if (pick_shape(p.M, true) == 3) {
+            if (QR_DUAL_CFG == 1) return launch_cfg<F, 2, 2, 2, 1, true>(p, st);
+            if (QR_DUAL_CFG == 2) return launch_cfg<F, 4, 2, 2, 1, true>(p, st);
+            if (QR_DUAL_CFG == 3) return launch_cfg<F, 2, 2, 2, 2, true>(p, st);
+            return launch_cfg<F, 4, 2, 1, 1, true>(p, st);
+        }
         return launch_cfg<F, 2, 2, 1, 1, true>(p, st);
     } else {
         switch (pick_shape(p.M, false)) {
