@@ -139,7 +139,7 @@ gemm_kernel(GemmParams p) {
             const bool up = DUAL && col >= C::BN;
             const int lcol = up ? col - C::BN : col;
             // out-of-range groups read as zeros (buffer bounds) and decode to zeros
-            const uint32_t coff = (tid + NT * u < C::UNITS && g < g_end) ? (uint32_t)lcol * col_bytes : kOOB;
+            const uint32_t coff = ((C::UNITS % NT == 0 || tid + NT * u < C::UNITS) && g < g_end) ? (uint32_t)lcol * col_bytes : kOOB;
             Dec::load(up ? wr1 : wr0, coff, coff == kOOB ? 0u : g, wraw[slot][u]);
         }
     };
@@ -150,7 +150,7 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < C::XPT; i++) {
             const int c = tid + NT * i;
-            if (c < C::XCH) {
+            if (C::XCH % NT == 0 || c < C::XCH) {
                 const int row = c >> 3, kc = c & 7;
                 *reinterpret_cast<u4_t*>(As + row * kLdsRow + kc * 8) =
                     u4_t{xraw[slot][i][0], xraw[slot][i][1], xraw[slot][i][2], xraw[slot][i][3]};
@@ -158,7 +158,7 @@ gemm_kernel(GemmParams p) {
         }
 #pragma unroll
         for (int u = 0; u < C::UPT; u++) {
-            if (tid + NT * u < C::UNITS) {
+            if (C::UNITS % NT == 0 || tid + NT * u < C::UNITS) {
                 int col, gsel, half;
                 unit_of(u, col, gsel, half);
                 const uint32_t g = g_begin + step * 2 + gsel;
@@ -166,12 +166,7 @@ gemm_kernel(GemmParams p) {
                 const uint32_t par = Dec::parity((uint32_t)lcol * col_bytes, g);
                 if (C::HALF) {
                     uint32_t out[8];
-#ifdef QR_GEMM_NODECODE  // timing experiment only: raw words instead of decoded weights
-#pragma unroll
-                    for (int q = 0; q < 8; q++) out[q] = wraw[slot][u][q % Dec::kRawWords] ^ par;
-#else
                     Dec::decode_half(wraw[slot][u], par, half, out);
-#endif
                     u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + gsel * 32 + half * 16);
                     dst[0] = u4_t{out[0], out[1], out[2], out[3]};
                     dst[1] = u4_t{out[4], out[5], out[6], out[7]};
@@ -243,20 +238,34 @@ gemm_kernel(GemmParams p) {
     if ((uint32_t)P < nsteps) load_step(P, 0);
     __syncthreads();
 
-    // ---- main loop, unrolled by P so register stages are static ----
-    for (uint32_t s0 = 0; s0 < nsteps; s0 += P) {
+    // ---- main loop, unrolled by P so register stages are static.  Full groups
+    // of P steps run branch-free (the last group's look-ahead fetches fall out
+    // of range and read zeros), so the MFMAs of step s, the decode and LDS
+    // stores of step s+1 and the fetches of step s+1+P form one basic block
+    // that the scheduler interleaves. ----
+    uint32_t s0 = 0;
+    for (; s0 + P <= nsteps; s0 += P) {
 #pragma unroll
         for (int j = 0; j < P; j++) {
             const uint32_t s = s0 + j;
-            if (s < nsteps) {
-                compute(s & 1);
-                if (s + 1 < nsteps) {
-                    const int slot = (j + 1) % P;
-                    store_step(s + 1, slot, (s + 1) & 1);
-                    if (s + 1 + P < nsteps) load_step(s + 1 + P, slot);
-                }
-                __syncthreads();
+            const int slot = (j + 1) % P;
+            compute(s & 1);
+            store_step(s + 1, slot, (s + 1) & 1);
+            load_step(s + 1 + P, slot);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        const uint32_t s = s0 + j;
+        if (s < nsteps) {
+            compute(s & 1);
+            if (s + 1 < nsteps) {
+                const int slot = (j + 1) % P;
+                store_step(s + 1, slot, (s + 1) & 1);
+                if (s + 1 + P < nsteps) load_step(s + 1 + P, slot);
             }
+            __syncthreads();
         }
     }
 
@@ -314,7 +323,75 @@ gemm_kernel(GemmParams p) {
     }
 
     // ---- epilogue: accumulator element r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
-    // column l%32 of the 32x32 MFMA tile ----
+    // column l%32 of the 32x32 MFMA tile.  The (SwiGLU-combined) fp32 values go
+    // through LDS, one 32-row band of the wave tile at a time, so that each
+    // lane then owns 8 consecutive columns of one row: the residual is read and
+    // the output written with 16-byte accesses, and the value is rounded to
+    // fp16 once, after the residual add. ----
+    auto value = [&](int i, int j, int r) {
+        float v = acc[i][j][r];
+        if constexpr (DUAL) {
+            const float u = acc2[i][j][r];
+            v = v / (1.0f + __expf(-v)) * u;
+        }
+        return v;
+    };
+    const bool vec_io = ((reinterpret_cast<uintptr_t>(p.Y) | reinterpret_cast<uintptr_t>(p.R)) & 15u) == 0 &&
+                        (N & 7u) == 0 && (p.head_D & 7u) == 0;
+    if (vec_io) {
+        constexpr int WC = TN * 32;        // wave tile columns
+        constexpr int ERS = WC + 4;        // padded LDS row (floats)
+        static_assert(WGM * WGN * 32 * ERS * 4 <= 2 * C::LDS_STAGE * 2, "epilogue staging fits the LDS stages");
+        float* E = reinterpret_cast<float*>(lds) + wave * 32 * ERS;
+        __syncthreads();  // every wave is done with the operand stages
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    E[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ERS + j * 32 + (lane & 31)] = value(i, j, r);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes done (wave-local region)
+            __builtin_amdgcn_wave_barrier();
+            constexpr int CHUNKS = 32 * WC / 8;  // 8-column chunks in the band
+#pragma unroll
+            for (int c = lane; c < CHUNKS; c += 64) {
+                const int row = c / (WC / 8), c8 = c % (WC / 8);
+                const int m = m0 + wm * TM * 32 + i * 32 + row;
+                const int n = n0 + wn * WC + c8 * 8;
+                if (m < (int)M && n < (int)N) {
+                    const f4_t lo = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8);
+                    const f4_t hi = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8 + 4);
+                    float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    if (p.R) {
+                        const u4_t rr = *reinterpret_cast<const u4_t*>(p.R + (size_t)m * N + n);
+                        const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const h2_t h = as_h2(rw[q]);
+                            v[2 * q] += (float)h.x;
+                            v[2 * q + 1] += (float)h.y;
+                        }
+                    }
+                    u4_t o;
+                    o.x = pack_h2(f2h_bits(v[0]), f2h_bits(v[1]));
+                    o.y = pack_h2(f2h_bits(v[2]), f2h_bits(v[3]));
+                    o.z = pack_h2(f2h_bits(v[4]), f2h_bits(v[5]));
+                    o.w = pack_h2(f2h_bits(v[6]), f2h_bits(v[7]));
+                    size_t off;
+                    if (p.head_D) {
+                        const uint32_t h = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
+                        off = ((size_t)h * M + m) * p.head_D + dd;
+                    } else {
+                        off = (size_t)m * N + n;
+                    }
+                    *reinterpret_cast<u4_t*>(p.Y + off) = o;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();  // band reads done before the next band overwrites
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -324,11 +401,7 @@ gemm_kernel(GemmParams p) {
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * TM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < (int)M && n < (int)N) {
-                    float v = acc[i][j][r];
-                    if constexpr (DUAL) {
-                        const float u = acc2[i][j][r];
-                        v = v / (1.0f + __expf(-v)) * u;
-                    }
+                    float v = value(i, j, r);
                     if (p.R) v += (float)p.R[(size_t)m * N + n];
                     size_t o;
                     if (p.head_D) {
