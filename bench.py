@@ -216,6 +216,22 @@ def bench_layer(b, timer, M, dm, H, D, Nm, seed):
             "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
 
 
+def bench_copy(timer, nbytes: int):
+    """Device-to-device copy of a known size: the calibration point for the
+    FETCH_SIZE / WRITE_SIZE counters (bytes moved = nbytes read + nbytes written)."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+
+    def step(i):
+        dst.copy_(src)
+
+    ms = timer.run(step)
+    return {"name": "copy_calib", "bytes": nbytes, "ms": round(ms, 5),
+            "gbs": round(2.0 * nbytes / (ms * 1e-3) / 1e9, 1), "timing": timer.mode}
+
+
 def cpu_baseline(fmt, X, Wn, N, seconds: float):
     """The oracle (CPU restatement of the reference's gold) on a growing row
     sample of the headline configuration until ~`seconds` of CPU work."""
@@ -272,6 +288,8 @@ def main():
         name = f"m2048_k4096_{tag}"
         if want is not None and name in want:
             per[name], _ = bench_projection(b, timer, name, fmt, 2048, 4096, 4096, 60 + fmt)
+    if want is not None and "copy_calib" in want:
+        per["copy_calib"] = bench_copy(timer, 256 << 20)
     if on("cfg5_swiglu"):
         per["cfg5_swiglu"] = bench_swiglu(b, timer, 2048, 2048, 8192, 50)
     if on("cfg5_attention"):

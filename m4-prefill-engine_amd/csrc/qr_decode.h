@@ -121,6 +121,24 @@ template <> struct Decoder<QUANT_Q4_K> {
         const int gap = binade(d16) - binade(dm16);
         fast = (A == 0.0f) || (B == 0.0f) || (gap <= 3 && gap >= -7);
     }
+    // Fast path only (caller has established that no lane needs the exact-sum path).
+    __device__ static void decode_half_fast(const uint32_t raw[8], uint32_t s, int h, uint32_t out[8]) {
+        float A, B;
+        bool fast;
+        scales(raw, s, A, B, fast);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t n = (h ? (raw[4 + i] >> 4) : raw[4 + i]) & 0x0f0f0f0fu;
+            out[2 * i + 0] = affine_pair_exact(nib_pair_lo(n), A, -B);
+            out[2 * i + 1] = affine_pair_exact(nib_pair_hi(n), A, -B);
+        }
+    }
+    __device__ static bool needs_exact(const uint32_t raw[8], uint32_t s) {
+        float A, B;
+        bool fast;
+        scales(raw, s, A, B, fast);
+        return !fast;
+    }
     __device__ static void decode_half(const uint32_t raw[8], uint32_t s, int h, uint32_t out[8]) {
         float A, B;
         bool fast;
@@ -179,6 +197,20 @@ template <> struct Decoder<QUANT_TERNARY_1_58> {
     }
     __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
 };
+
+// Branch-free half-group decode for pipelined callers: bit-exact whenever no
+// lane of the wave has needs_exact() true for its group (only Q4_K has a slow
+// path; its callers check and re-decode with decode_group otherwise).
+template <int F>
+__device__ __forceinline__ void decode_half_fast(const uint32_t* raw, uint32_t parity, int h, uint32_t out[8]) {
+    if constexpr (F == QUANT_Q4_K) Decoder<F>::decode_half_fast(raw, parity, h, out);
+    else Decoder<F>::decode_half(raw, parity, h, out);
+}
+template <int F>
+__device__ __forceinline__ bool needs_exact(const uint32_t* raw, uint32_t parity) {
+    if constexpr (F == QUANT_Q4_K) return Decoder<F>::needs_exact(raw, parity);
+    else return false;
+}
 
 // Whole group: words 0..15.
 template <int F>

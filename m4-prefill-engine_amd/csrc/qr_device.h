@@ -35,6 +35,12 @@ __device__ __forceinline__ u4_t ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
+// Bit casts through by-value parameters.  (This toolchain's clang miscompiles
+// __builtin_bit_cast applied directly to an ext_vector element such as v.y:
+// every element reads as element 0.)
+__device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+
 __device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 __device__ __forceinline__ uint32_t as_u32(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ float h2f(uint32_t bits16) {

@@ -31,6 +31,8 @@
 #include "qr_decode.h"
 #include "qr_kernels.h"
 
+#include <stdlib.h>
+
 namespace qr {
 
 constexpr int kBK = 64;
@@ -460,7 +462,19 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Kernel selection: the register-B kernel (qr_gemm_rb.hip) unless
+// QR_GEMM_IMPL=lds selects the LDS-staged one.
+static bool use_rb() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("QR_GEMM_IMPL");
+        v = (e && e[0] == 'l') ? 0 : 1;
+    }
+    return v == 1;
+}
+
 uint32_t gemm_pick_ksplit(const GemmParams& p) {
+    if (use_rb()) return gemm_rb_pick_ksplit(p);
     const bool dual = p.W2 != nullptr;
     if (dual) return 1;
     uint32_t bm, bn;
@@ -474,6 +488,7 @@ uint32_t gemm_pick_ksplit(const GemmParams& p) {
 }
 
 size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
+    if (use_rb()) return gemm_rb_workspace_floats(p, ks, tiles);
     uint32_t bm, bn;
     const bool dual = p.W2 != nullptr;
     shape_dims(pick_shape(p.M, dual), bm, bn);
@@ -504,7 +519,13 @@ static hipError_t launch_fmt(const GemmParams& p, hipStream_t st) {
     }
 }
 
-hipError_t launch_gemm(const GemmParams& p, hipStream_t st) {
+hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
+    if (use_rb()) {
+        GemmParams p = p0;
+        p.group_m = gemm_rb_group_m(p);
+        return launch_gemm_rb(p, st);
+    }
+    const GemmParams& p = p0;
     const bool dual = p.W2 != nullptr;
     switch (p.format) {
         case QUANT_Q4_0: return dual ? launch_fmt<QUANT_Q4_0, true>(p, st) : launch_fmt<QUANT_Q4_0, false>(p, st);

@@ -1,0 +1,603 @@
+// qr_gemm_rb.hip -- quantized projection Y = X . W^T on gfx950 MFMA, weights
+// decoded straight into MFMA B-operand registers (tiled, M > 64).
+//
+// Replaces the reference's block_mma_64x64_engine (quant_router_kernels.metal:
+// 442-581) with its entry points (:588-927), and the fused dual-projection
+// SwiGLU swiglu_mma_dual_simd (brick3_swiglu_kernels.metal:428-698).
+//
+// One workgroup = NW wave64s and one BM x BN output tile (BM = 32 TM rows,
+// BN = NW x 32 TN columns).  The waves split the tile along N only, so every
+// weight column belongs to exactly one wave and is decoded exactly once per
+// workgroup:
+//  * K advances 64 per step = two 32-element quant groups per column.  For
+//    v_mfma_f32_32x32x16_f16 lane l supplies column l % 32 and the 8 k values
+//    8 (l / 32) .. +7 of each 16-wide slice; here the K order inside a step is
+//    permuted so that lane half h = l / 32 owns quant group h of the step
+//    whole: at slice kk the lane holds elements 8 kk .. 8 kk + 7 of its group.
+//    The sum over k is order-free, so X (the A operand) is read with the same
+//    permutation: row r, k = 32 h + 8 kk + i.
+//  * Each lane fetches the raw block of its (column, group) with buffer loads
+//    P steps ahead and decodes all 32 weights to binary16 in registers
+//    (qr_decode.h: bit-exact vs the CPU unpack).  No LDS traffic for weights.
+//  * The X tile [BM x 64] fp16 is fetched with 16-byte buffer loads (P steps
+//    ahead) into a double-buffered LDS stage, padded 8 halfs per row so the
+//    ds_read_b128 fragment reads are bank-conflict free; one barrier per step.
+//    Per step a wave reads BM x 64 x 2 bytes of LDS for BM x 32 TN x 64 x 2
+//    flop: with TN = 2 that is half the LDS bandwidth at full MFMA rate.
+//  * The MFMAs of step s, the decode of step s + 1 and the fetches of step
+//    s + 1 + P sit in one basic block (the main loop is unrolled by P and
+//    branch-free), so decode VALU work issues under the matrix pipe.
+//  * XCD-aware tile order (consecutive workgroup ids land on different XCDs):
+//    each XCD gets a contiguous run of tiles, grouped GM row-tiles x many
+//    column-tiles so X rows and weight columns are reused from its L2.
+//  * Epilogue: fp32 accumulators (+ fp16 residual, + SwiGLU for the dual
+//    variant) rounded once to fp16, staged through LDS for 16-byte stores,
+//    written [M, N] or head-major [H, M, D] (quant_router_kernels.metal:570-574).
+//    K split across workgroups: partials go to a workspace with agent-scope
+//    stores; the last workgroup of the tile (agent-scope counter) sums them in
+//    split order -- deterministic, one launch.
+#include "qr_decode.h"
+#include "qr_kernels.h"
+
+namespace qr {
+
+#ifndef QR_RB_STAGES
+#define QR_RB_STAGES 2
+#endif
+#ifndef QR_RB_VPM
+#define QR_RB_VPM 5
+#endif
+
+#ifdef QR_RB_TRACE
+__device__ unsigned long long qr_rb_trace[8 * 65536];
+#define RB_TRACE_EXIT() do { if (threadIdx.x == 0) qr_rb_trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + 4] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define RB_TRACE_EXIT() ((void)0)
+#endif
+
+namespace rb {
+
+constexpr int kBK = 64;
+constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
+
+template <int TM, int TN, int NW, bool DUAL>
+struct Cfg {
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 32 * TM;
+    static constexpr int WN = 32 * TN;            // columns per wave
+    static constexpr int BN = NW * WN;
+    static constexpr int NCB = DUAL ? 2 * TN : TN;  // 32-column B tiles per wave (gate, then up)
+    static constexpr int XCH = BM * kBK / 8;      // 16-byte X chunks per step
+    static constexpr int XPT = (XCH + NT - 1) / NT;
+    static constexpr int LDS_STAGE = BM * kLdsRow;  // halfs
+    static constexpr int ACC = TM * NCB * 16;     // accumulator floats per lane
+    static constexpr int EPI_BYTES = NW * 32 * (WN + 4) * 4;  // epilogue staging
+    static constexpr int LDS_BYTES = 3 * LDS_STAGE * 2 > EPI_BYTES ? 3 * LDS_STAGE * 2 : EPI_BYTES;
+};
+
+__device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t gm_req, uint32_t& tm,
+                                        uint32_t& tn) {
+    const uint32_t T = nt_m * nt_n;
+    uint32_t t = bid;
+    if (T % 8 == 0) t = (bid % 8) * (T / 8) + bid / 8;
+    const uint32_t GM = gm_req ? gm_req : 2;
+    const uint32_t per_group = GM * nt_n;
+    const uint32_t grp = t / per_group;
+    const uint32_t first = grp * GM;
+    const uint32_t gm = min(GM, nt_m - first);
+    const uint32_t in = t % per_group;
+    tm = first + in % gm;
+    tn = in / gm;
+}
+
+}  // namespace rb
+
+template <int F, int TM, int TN, int NW, bool DUAL, int P>
+__global__ void __launch_bounds__(64 * NW)
+gemm_rb_kernel(GemmParams p) {
+    using C = rb::Cfg<TM, TN, NW, DUAL>;
+    using Dec = Decoder<F>;
+    constexpr int NT = C::NT;
+    constexpr int NCB = C::NCB;
+    constexpr int kBK = rb::kBK;
+    constexpr int kLdsRow = rb::kLdsRow;
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = lane >> 5;     // quant group of the step this lane owns
+#ifdef QR_RB_TRACE
+    const size_t trace_id = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8;
+    if (tid == 0) {
+        qr_rb_trace[trace_id] = __builtin_amdgcn_s_memtime();
+        qr_rb_trace[trace_id + 1] = __builtin_amdgcn_s_memrealtime();
+    }
+#endif
+    const int c32 = lane & 31;
+
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t nt_m = (M + C::BM - 1) / C::BM, nt_n = (N + C::BN - 1) / C::BN;
+    uint32_t tmi, tni;
+    rb::tile_of(blockIdx.x, nt_m, nt_n, p.group_m, tmi, tni);
+    const int m0 = tmi * C::BM, n0 = tni * C::BN;
+    const uint32_t ksplit = p.ksplit ? p.ksplit : 1;
+    const uint32_t kz = blockIdx.y;
+    const uint32_t Kc = K / ksplit;  // host guarantees divisibility (and Kc % 32 == 0)
+    const uint32_t k_begin = kz * Kc, k_end = k_begin + Kc;
+    const uint32_t nsteps = (Kc + kBK - 1) / kBK;
+    const uint32_t g_begin = k_begin / 32, g_end = k_end / 32;
+    const uint32_t col_bytes = (uint32_t)p.col_bytes;
+
+    const int mrows = min(C::BM, (int)M - m0);
+    const int ncols = min(C::BN, (int)N - n0);
+    auto xr = make_rsrc(p.X + (size_t)m0 * K, (uint32_t)mrows * K * 2u);
+    auto wr0 = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
+    auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
+
+    // local column of B tile jb for this lane
+    auto bcol = [&](int jb) { return wave * C::WN + (jb % TN) * 32 + c32; };
+
+    // Pipelines (U = 6 steps unrolled, so every ring index below is static):
+    //  X:  raw 16-byte chunks fetched 4 steps ahead into XP = 2 register slots,
+    //      written to LDS 2 steps ahead into a 3-stage ring;
+    //  A:  fragments of slice kk + 1 read while slice kk multiplies; the first
+    //      slice of step s + 1 is read before the step's barrier (its stage was
+    //      written before the previous barrier);
+    //  W:  raw blocks fetched WP steps ahead, decoded one step ahead into the
+    //      two B buffers.
+    constexpr int XS = 3, XP = 2, WP = P, U = 6;
+    static_assert(U % XS == 0 && U % XP == 0 && U % WP == 0, "ring sizes divide the unroll");
+    uint32_t xraw[XP][C::XPT][4];
+    uint32_t wraw[WP][NCB][Dec::kRawWords];
+
+    auto load_x = [&](uint32_t step, int slot) {
+        const uint32_t k0 = k_begin + step * kBK;
+#pragma unroll
+        for (int i = 0; i < C::XPT; i++) {
+            const int c = tid + NT * i;
+            const int row = c >> 3, kc = c & 7;
+            const uint32_t k = k0 + kc * 8;  // past the range (or the last step): zeros
+            const uint32_t off = ((C::XCH % NT == 0 || c < C::XCH) && k < k_end) ? ((uint32_t)row * K + k) * 2u : kOOB;
+#ifdef QR_RB_NOX
+            const u4_t v = u4_t{off, off, off, off};
+#else
+            const u4_t v = ld_b128(xr, off);
+#endif
+            xraw[slot][i][0] = v.x; xraw[slot][i][1] = v.y; xraw[slot][i][2] = v.z; xraw[slot][i][3] = v.w;
+        }
+    };
+    auto load_w = [&](uint32_t step, int slot) {
+        const uint32_t g = g_begin + step * 2 + h;
+        const bool live = g < g_end;
+#pragma unroll
+        for (int jb = 0; jb < NCB; jb++) {
+            const uint32_t coff = live ? (uint32_t)bcol(jb) * col_bytes : kOOB;
+#ifdef QR_RB_NOWLOAD
+            for (int q = 0; q < Dec::kRawWords; q++) wraw[slot][jb][q] = coff + q + g;
+#else
+            Dec::load((DUAL && jb >= TN) ? wr1 : wr0, coff, live ? g : 0u, wraw[slot][jb]);
+#endif
+        }
+    };
+
+    auto store_x = [&](int slot, int stage) {
+        _Float16* As = lds + stage * C::LDS_STAGE;
+#pragma unroll
+        for (int i = 0; i < C::XPT; i++) {
+            const int c = tid + NT * i;
+            if (C::XCH % NT == 0 || c < C::XCH) {
+                const int row = c >> 3, kc = c & 7;
+                *reinterpret_cast<u4_t*>(As + row * kLdsRow + kc * 8) =
+                    u4_t{xraw[slot][i][0], xraw[slot][i][1], xraw[slot][i][2], xraw[slot][i][3]};
+            }
+        }
+    };
+
+    auto decode = [&](uint32_t step, int slot, uint32_t out[NCB][16]) {
+        const uint32_t g = g_begin + step * 2 + h;
+#pragma unroll
+        for (int jb = 0; jb < NCB; jb++) {
+            const uint32_t par = Dec::parity((uint32_t)bcol(jb) * col_bytes, g);
+#ifdef QR_RB_NODECODE
+            for (int q = 0; q < 16; q++) out[jb][q] = wraw[slot][jb][q % Dec::kRawWords] ^ par;
+#else
+            decode_group<F>(wraw[slot][jb], par, out[jb]);
+#endif
+        }
+    };
+
+    f16v_t acc[TM][NCB];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < NCB; j++) acc[i][j] = f16v_t{};
+
+    const int arow = c32;
+    const int akof = 32 * h;
+    auto read_a = [&](int stage, int kk, h8_t out[TM]) {
+        const _Float16* As = lds + stage * C::LDS_STAGE;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#ifdef QR_RB_NOA
+            out[i] = h8_t{(_Float16)(stage + kk), (_Float16)i, 0, 0, 0, 0, 0, (_Float16)1};
+#else
+            out[i] = *reinterpret_cast<const h8_t*>(As + (arow + i * 32) * kLdsRow + akof + kk * 8);
+#endif
+    };
+
+    uint32_t bw[2][NCB][16];
+    h8_t af[2][TM];
+
+    // One K step, as four k-slices.  Slice kk: read the A fragments of slice
+    // kk + 1 (of step s + 1 for the last slice), the TM x NCB MFMAs of slice kk,
+    // one half-group decode of step s + 1 and a share of the memory traffic
+    // (W fetch of step s + 1 + WP, X store of step s + 2, X fetch of step s + 4).
+    // Each slice is a fenced scheduling region in which MFMAs and decode VALU
+    // ops alternate, so the decode issues while the matrix pipe is busy.
+    constexpr int NM = TM * NCB;            // MFMAs per slice
+    constexpr int HALVES = 2 * NCB;         // half-group decodes per step
+    static_assert(HALVES <= 4, "at most one half decode per slice");
+    auto step_body = [&](uint32_t s, int j) {
+        const int wslot = (j + 1) % WP;
+        uint32_t (*bn)[16] = bw[(j + 1) & 1];
+        const uint32_t gn = g_begin + (s + 1) * 2 + h;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk < 3) read_a(j % XS, kk + 1, af[(kk + 1) & 1]);
+            else read_a((j + 1) % XS, 0, af[0]);
+#pragma unroll
+            for (int jb = 0; jb < NCB; jb++) {
+                const uint32_t* bj = bw[j & 1][jb];
+                const h8_t b = __builtin_bit_cast(h8_t, u4_t{bj[4 * kk], bj[4 * kk + 1], bj[4 * kk + 2], bj[4 * kk + 3]});
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#ifdef QR_RB_NOMFMA
+                    acc[i][jb][0] += (float)af[kk & 1][i][0] * (float)b[0];
+#else
+                    acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], b, acc[i][jb], 0, 0, 0);
+#endif
+            }
+            if (kk < HALVES) {
+                const int jb = kk >> 1, hh = kk & 1;
+                const uint32_t par = Dec::parity((uint32_t)bcol(jb) * col_bytes, gn);
+#ifdef QR_RB_NODECODE
+                for (int q = 0; q < 8; q++) bn[jb][8 * hh + q] = wraw[wslot][jb][q % Dec::kRawWords] ^ par;
+#else
+                decode_half_fast<F>(wraw[wslot][jb], par, hh, bn[jb] + 8 * hh);
+#endif
+            }
+            if (kk == 1) store_x((j + 2) % XP, (j + 2) % XS);
+            if (kk == 2) load_x(s + 2 + XP, (j + 2) % XP);
+#ifndef QR_RB_NOSCHED
+            __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);  // DS read
+#pragma unroll
+            for (int q = 0; q < NM; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, QR_RB_VPM, 0);  // VALU
+            }
+#endif
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (F == QUANT_Q4_K) {
+            bool slow = false;
+#pragma unroll
+            for (int jb = 0; jb < NCB; jb++)
+                slow |= needs_exact<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn));
+            if (__any(slow)) {
+#pragma unroll
+                for (int jb = 0; jb < NCB; jb++)
+                    decode_group<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn), bn[jb]);
+            }
+        }
+        load_w(s + 1 + WP, wslot);
+#ifndef QR_RB_NOSYNC
+        __syncthreads();
+#endif
+    };
+
+    // ---- prologue ----
+#pragma unroll
+    for (int t = 0; t < XP; t++) load_x(t, t);
+#pragma unroll
+    for (int t = 0; t < WP; t++) load_w(t, t);
+    store_x(0, 0);
+    store_x(1, 1);
+    load_x(XP, 0);
+    load_x(XP + 1, 1);
+    decode(0, 0, bw[0]);
+    load_w(WP, 0);
+    __syncthreads();
+    read_a(0, 0, af[0]);
+
+    // ---- main loop: full groups of U steps branch-free (look-ahead fetches past
+    // the K range read zeros), then the remainder with guards ----
+    uint32_t s0 = 0;
+    for (; s0 + U <= nsteps; s0 += U) {
+#pragma unroll
+        for (int j = 0; j < U; j++) step_body(s0 + j, j);
+    }
+#pragma unroll
+    for (int j = 0; j < U; j++)
+        if (s0 + j < nsteps) step_body(s0 + j, j);
+
+#ifdef QR_RB_TRACE
+    if (tid == 0) {
+        qr_rb_trace[trace_id + 2] = __builtin_amdgcn_s_memtime();
+        qr_rb_trace[trace_id + 3] = __builtin_amdgcn_s_memrealtime();
+    }
+#endif
+    // ---- split-K: publish partials, the last workgroup of the tile sums ----
+    // Workspace slot of (split z, tile): ACC / 2 float pairs per thread, pair q
+    // of thread t at q * NT + t (coalesced across lanes).  Partials cross XCDs,
+    // whose L2s are not coherent with each other: they are written and read
+    // with 64-bit agent-scope atomics (write-through / read-from-memory); the
+    // reads are issued in batches of up to 32 so their latencies overlap.
+    if (ksplit > 1) {
+        constexpr int NP = C::ACC / 2;                 // float pairs per thread
+        constexpr int BATCH = NP < 32 ? NP : 32;       // pairs in flight per batch
+        static_assert(NP % BATCH == 0 && BATCH % 8 == 0, "whole 32x32 tiles per batch");
+        const uint32_t T = nt_m * nt_n;
+        const uint32_t tile = tmi * nt_n + tni;
+        auto pair_ptr = [&](uint32_t z) {
+            return reinterpret_cast<uint64_t*>(p.ws) + ((size_t)z * T + tile) * (NP * NT) + tid;
+        };
+        {
+            uint64_t* dst = pair_ptr(kz);
+            int q = 0;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < NCB; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2, q++) {
+                        const uint64_t v = (uint64_t)f32_bits(acc[i][j][r]) | ((uint64_t)f32_bits(acc[i][j][r + 1]) << 32);
+                        __hip_atomic_store(dst + q * NT, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
+        __syncthreads();
+        __shared__ uint32_t s_last;
+        if (tid == 0) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = (prev == ksplit - 1) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!s_last) { RB_TRACE_EXIT(); return; }
+        // sum all splits in split order (deterministic)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < NCB; j++) acc[i][j] = f16v_t{};
+        for (uint32_t z = 0; z < ksplit; z++) {
+            const uint64_t* src = pair_ptr(z);
+#pragma unroll
+            for (int q0 = 0; q0 < NP; q0 += BATCH) {
+                uint64_t t[BATCH];
+#pragma unroll
+                for (int q = 0; q < BATCH; q++)
+                    t[q] = __hip_atomic_load(src + (q0 + q) * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int q = 0; q < BATCH; q++) {
+                    const int qq = q0 + q;               // pair index: tile qq / 8, rows 2 (qq % 8)
+                    const int i = (qq / 8) / NCB, j = (qq / 8) % NCB, r = 2 * (qq % 8);
+                    acc[i][j][r] += bits_f32((uint32_t)t[q]);
+                    acc[i][j][r + 1] += bits_f32((uint32_t)(t[q] >> 32));
+                }
+            }
+        }
+        if (tid == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- epilogue: accumulator element r of lane l is row 8 (r / 4) + 4 (l / 32)
+    // + r % 4, column l % 32 of its 32x32 tile.  Values (SwiGLU-combined) go
+    // through LDS one 32-row band of the wave tile at a time, so each lane then
+    // owns 8 consecutive columns of one row: residual read and output written
+    // with 16-byte accesses, one rounding to fp16 after the residual add. ----
+    auto value = [&](int i, int j, int r) {
+        float v = acc[i][j][r];
+        if constexpr (DUAL) {
+            const float u = acc[i][j + TN][r];
+            v = v / (1.0f + __expf(-v)) * u;
+        }
+        return v;
+    };
+    const int wcol0 = n0 + wave * C::WN;
+    const bool vec_io = ((reinterpret_cast<uintptr_t>(p.Y) | reinterpret_cast<uintptr_t>(p.R)) & 15u) == 0 &&
+                        (N & 7u) == 0 && (p.head_D & 7u) == 0;
+    if (vec_io) {
+        constexpr int WC = C::WN;
+        constexpr int ERS = WC + 4;  // padded LDS row (floats)
+        static_assert(NW * 32 * ERS * 4 <= C::LDS_BYTES, "epilogue staging fits the LDS allocation");
+        float* E = reinterpret_cast<float*>(lds) + wave * 32 * ERS;
+        __syncthreads();  // every wave is done with the X stages
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    E[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ERS + j * 32 + c32] = value(i, j, r);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes done (wave-local region)
+            __builtin_amdgcn_wave_barrier();
+            constexpr int CHUNKS = 32 * WC / 8;
+#pragma unroll
+            for (int c = lane; c < CHUNKS; c += 64) {
+                const int row = c / (WC / 8), c8 = c % (WC / 8);
+                const int m = m0 + i * 32 + row;
+                const int n = wcol0 + c8 * 8;
+                if (m < (int)M && n < (int)N) {
+                    const f4_t lo = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8);
+                    const f4_t hi = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8 + 4);
+                    float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    if (p.R) {
+                        const u4_t rr = *reinterpret_cast<const u4_t*>(p.R + (size_t)m * N + n);
+                        const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const h2_t hh = as_h2(rw[q]);
+                            v[2 * q] += (float)hh.x;
+                            v[2 * q + 1] += (float)hh.y;
+                        }
+                    }
+                    u4_t o;
+                    o.x = pack_h2(f2h_bits(v[0]), f2h_bits(v[1]));
+                    o.y = pack_h2(f2h_bits(v[2]), f2h_bits(v[3]));
+                    o.z = pack_h2(f2h_bits(v[4]), f2h_bits(v[5]));
+                    o.w = pack_h2(f2h_bits(v[6]), f2h_bits(v[7]));
+                    size_t off;
+                    if (p.head_D) {
+                        const uint32_t hd = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
+                        off = ((size_t)hd * M + m) * p.head_D + dd;
+                    } else {
+                        off = (size_t)m * N + n;
+                    }
+                    *reinterpret_cast<u4_t*>(p.Y + off) = o;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();  // band reads done before the next band overwrites
+        }
+        RB_TRACE_EXIT();
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = wcol0 + j * 32 + c32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < (int)M && n < (int)N) {
+                    float v = value(i, j, r);
+                    if (p.R) v += (float)p.R[(size_t)m * N + n];
+                    size_t o;
+                    if (p.head_D) {
+                        const uint32_t hd = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
+                        o = ((size_t)hd * M + m) * p.head_D + dd;
+                    } else {
+                        o = (size_t)m * N + n;
+                    }
+                    p.Y[o] = (_Float16)v;
+                }
+            }
+        }
+}
+
+
+// Shapes {TM, TN, NW}: BM = 32 TM, BN = 32 TN NW.
+//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K: QR_RB_BIG_K,
+//                  default 4, 1, 8 -> 128 x 256 with two waves per SIMD, whose
+//                  heavier decode then overlaps the other wave's MFMAs)
+//   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
+//                  of 128 x 256 at the same K split, half the reduction)
+//   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
+#ifndef QR_RB_BIG
+#define QR_RB_BIG 4, 2, 4
+#endif
+#ifndef QR_RB_BIG_K
+#define QR_RB_BIG_K 4, 1, 8
+#endif
+#ifndef QR_RB_MID
+#define QR_RB_MID 4, 1, 4
+#endif
+template <int TM, int TN, int NW> struct ShapeOf {
+    static constexpr uint32_t bm = 32 * TM, bn = 32 * TN * NW;
+};
+struct RbShape {
+    uint32_t bm, bn;
+};
+static int rb_pick(int format, uint32_t M, bool dual) {
+    if (dual) return 2;
+    if (M >= 1024) return format == QUANT_Q4_K ? 3 : 0;
+    return 1;
+}
+static RbShape rb_dims(int s) {
+    switch (s) {
+        case 0: return {ShapeOf<QR_RB_BIG>::bm, ShapeOf<QR_RB_BIG>::bn};
+        case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
+        case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
+        default: return {128, 128};
+    }
+}
+
+template <int F, int TM, int TN, int NW, bool DUAL>
+static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
+    using C = rb::Cfg<TM, TN, NW, DUAL>;
+    auto kern = gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES>;
+    const size_t lds = C::LDS_BYTES;
+    const uint32_t T = ((p.M + C::BM - 1) / C::BM) * ((p.N + C::BN - 1) / C::BN);
+    const uint32_t ks = p.ksplit ? p.ksplit : 1;
+    hipLaunchKernelGGL(kern, dim3(T, ks), dim3(C::NT), lds, st, p);
+    return hipGetLastError();
+}
+
+template <int F, bool DUAL>
+static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
+    if constexpr (DUAL) {
+        return rb_launch_cfg<F, 4, 1, 4, true>(p, st);
+    } else {
+        switch (rb_pick(F, p.M, false)) {
+            case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);
+            case 3: return rb_launch_cfg<F, QR_RB_BIG_K, false>(p, st);
+            default: return rb_launch_cfg<F, QR_RB_MID, false>(p, st);
+        }
+    }
+}
+
+hipError_t launch_gemm_rb(const GemmParams& p, hipStream_t st) {
+    const bool dual = p.W2 != nullptr;
+    switch (p.format) {
+        case QUANT_Q4_0: return dual ? rb_launch_fmt<QUANT_Q4_0, true>(p, st) : rb_launch_fmt<QUANT_Q4_0, false>(p, st);
+        case QUANT_MLX_4BIT: return dual ? rb_launch_fmt<QUANT_MLX_4BIT, true>(p, st) : rb_launch_fmt<QUANT_MLX_4BIT, false>(p, st);
+        case QUANT_Q4_K: return dual ? rb_launch_fmt<QUANT_Q4_K, true>(p, st) : rb_launch_fmt<QUANT_Q4_K, false>(p, st);
+        case QUANT_TERNARY_1_58: return dual ? rb_launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : rb_launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+uint32_t gemm_rb_pick_ksplit(const GemmParams& p) {
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
+    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+    // One workgroup fits a CU (its registers), so the grid runs in waves of
+    // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
+    // >= 512 of K per split) while the grid still fits one such wave.
+    uint32_t ks = 1;
+    while (T * ks * 2 <= 256 && p.K % (256 * ks * 2) == 0 && p.K / (ks * 2) >= 512) ks *= 2;
+    return ks;
+}
+
+size_t gemm_rb_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
+    const bool dual = p.W2 != nullptr;
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, dual));
+    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+    if (tiles) *tiles = T;
+    return ks > 1 ? (size_t)ks * T * d.bm * d.bn * (dual ? 2 : 1) : 0;
+}
+
+uint32_t gemm_rb_group_m(const GemmParams& p) {
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
+    const uint32_t nt_m = (p.M + d.bm - 1) / d.bm;
+    return nt_m >= 4 ? 4u : 2u;
+}
+
+}  // namespace qr
+
+#ifdef QR_RB_TRACE
+__global__ void qr_rb_stamp_kernel(int idx) {
+    qr::qr_rb_trace[8 * 65536 - 1 - idx] = __builtin_amdgcn_s_memrealtime();
+}
+extern "C" __attribute__((visibility("default"))) int qr_rb_stamp(int idx, hipStream_t st) {
+    hipLaunchKernelGGL(qr_rb_stamp_kernel, dim3(1), dim3(1), 0, st, idx);
+    return (int)hipGetLastError();
+}
+extern "C" __attribute__((visibility("default"))) int qr_rb_trace_read_tail(unsigned long long* out, int n) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(qr::qr_rb_trace), sizeof(unsigned long long) * n,
+                                    sizeof(unsigned long long) * (8 * 65536 - n));
+}
+extern "C" __attribute__((visibility("default"))) int qr_rb_trace_read(unsigned long long* out, int n) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(qr::qr_rb_trace), sizeof(unsigned long long) * n);
+}
+#endif
