@@ -216,6 +216,27 @@ def bench_layer(b, timer, M, dm, H, D, Nm, seed):
             "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
 
 
+def bench_fp16_reference(timer, name, M, K, N):
+    """Calibration point, not a router kernel: the vendor library's unquantized
+    fp16 GEMM (torch.matmul -> hipBLASLt) of the same shape, weights rotated the
+    same way.  It shows what an fp16 GEMM without any decode reaches here."""
+    import torch
+
+    X = torch.randn(M, K, dtype=torch.float16, device="cuda")
+    W0 = (torch.randn(N, K, dtype=torch.float16, device="cuda") * 0.02)
+    Ws = rotated(W0, W0.numel() * 2)
+    Y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+
+    def step(i):
+        torch.matmul(X, Ws[i % len(Ws)].t(), out=Y)
+
+    ms = timer.run(step)
+    tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"name": name, "M": M, "K": K, "N": N, "ms": round(ms, 5), "tflops": round(tf, 2),
+            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "timing": timer.mode,
+            "note": "unquantized fp16 torch.matmul (hipBLASLt) reference, not part of the router path"}
+
+
 def bench_copy(timer, nbytes: int):
     """Device-to-device copy of a known size: the calibration point for the
     FETCH_SIZE / WRITE_SIZE counters (bytes moved = nbytes read + nbytes written)."""
@@ -230,6 +251,20 @@ def bench_copy(timer, nbytes: int):
     ms = timer.run(step)
     return {"name": "copy_calib", "bytes": nbytes, "ms": round(ms, 5),
             "gbs": round(2.0 * nbytes / (ms * 1e-3) / 1e9, 1), "timing": timer.mode}
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch of the headline kernel, as measured by the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
+    profiles/gemm_rb_mlx_m128_traffic.md (copy-calibrated); None if absent."""
+    path = ROOT / "profiles" / "gemm_rb_mlx_m128_traffic.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith(f"traffic_bytes_per_launch {name}:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(fmt, X, Wn, N, seconds: float):
@@ -288,6 +323,10 @@ def main():
         name = f"m2048_k4096_{tag}"
         if want is not None and name in want:
             per[name], _ = bench_projection(b, timer, name, fmt, 2048, 4096, 4096, 60 + fmt)
+    for name, (M, K, N) in (("ref_fp16_gemm_m128_k4096_n14336", (128, 4096, 14336)),
+                            ("ref_fp16_gemm_m2048_k4096_n4096", (2048, 4096, 4096))):
+        if on(name):
+            per[name] = bench_fp16_reference(timer, name, M, K, N)
     if want is not None and "copy_calib" in want:
         per["copy_calib"] = bench_copy(timer, 256 << 20)
     if on("cfg5_swiglu"):
@@ -298,6 +337,7 @@ def main():
         per["cfg5_layer"] = bench_layer(b, timer, 2048, 2048, 32, 64, 8192, 52)
 
     head = per.get("cfg2_mlx_m128") or next(iter(per.values()))
+    traffic = traffic_from_profile("cfg2_mlx_m128") if "cfg2_mlx_m128" in per else None
     out = {
         "metric": "ms + effective TFLOPS per quantized projection at M=33/128/2048, K=4096",
         "value": head["tflops"],
@@ -314,7 +354,7 @@ def main():
         "config": {"workload": "MLX-4bit affine projection M=128 K=4096 N=14336 (BASELINE configs[1])",
                    "M": 128, "K": 4096, "N": 14336, "format": "MLX_4BIT (g64 repacked to 32-blocks)"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": None,
+                     "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": traffic,
                      "kernel": "gemm_kernel<QUANT_MLX_4BIT>", "hbm_frac": head.get("frac_hbm")},
         "per_config": per,
     }
