@@ -29,8 +29,11 @@ template <int F> struct Decoder;
 // --------------------------------------------------------------------------
 // Q4_0: 18-byte blocks, only 2-byte aligned inside a column.  Five aligned
 // dwords cover the block at either parity; the 16 code bytes are re-aligned
-// with a byte funnel shift.  Weights: (1024 + q - 1032) * d in binary16 --
-// the subtraction is exact and the product rounds once.
+// with a byte funnel shift.  Weights: (q - 8) * d in binary16 (q - 8 exact, one
+// rounding).  The GEMM kernels use decode_half_fast instead: fma(q, d, -8 d),
+// also one rounding of the exact value, one instruction less per pair; it
+// differs only in the sign of a zero weight (q = 8 with d < 0 gives +0, the
+// CPU unpack -0), which changes no product sum.
 // --------------------------------------------------------------------------
 template <> struct Decoder<QUANT_Q4_0> {
     static constexpr int kBlockElems = 32;
@@ -41,17 +44,46 @@ template <> struct Decoder<QUANT_Q4_0> {
 #pragma unroll
         for (int i = 0; i < 5; i++) raw[i] = ld_b32(r, a + 4u * i);
     }
-    __device__ static void decode_half(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
-        const uint32_t d16 = parity2 ? (raw[0] >> 16) : (raw[0] & 0xffffu);  // block at byte 2 of raw[0]?
+    __device__ static uint32_t scale_bits(const uint32_t raw[5], uint32_t parity2) {
+        return parity2 ? (raw[0] >> 16) : (raw[0] & 0xffffu);  // block at byte 2 of raw[0]?
+    }
+    __device__ static uint32_t codes(const uint32_t raw[5], uint32_t parity2, int i) {
+        return parity2 ? raw[i + 1] : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
+    }
+    // GEMM operand path: fma(q, d, -8 d) -- -8 d is exact and the fused op
+    // rounds once.  Valid while -8 d is finite (|d| <= 8188); needs_exact()
+    // flags the rest.  Zero weights come out +0 (see above).
+    __device__ static void decode_half_fast(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
+        const uint32_t d16 = scale_bits(raw, parity2);
         const h2_t d = as_h2(d16 | (d16 << 16));
-        const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+        const h2_t m8 = {(_Float16)-8.0f, (_Float16)-8.0f};
+        const h2_t c = d * m8;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t q = parity2 ? raw[i + 1] : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
+            const uint32_t q = codes(raw, parity2, i);
             const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
-            out[2 * i + 0] = as_u32((as_h2(nib_pair_lo(n)) - off) * d);
-            out[2 * i + 1] = as_u32((as_h2(nib_pair_hi(n)) - off) * d);
+            out[2 * i + 0] = as_u32(__builtin_elementwise_fma(code_pair<false>(n), d, c));
+            out[2 * i + 1] = as_u32(__builtin_elementwise_fma(code_pair<true>(n), d, c));
         }
+    }
+    // Any scale: (q - 8) exact in binary16, one rounding in the product.
+    __device__ static void decode_half_exact(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
+        const uint32_t d16 = scale_bits(raw, parity2);
+        const h2_t d = as_h2(d16 | (d16 << 16));
+        const h2_t off = {(_Float16)8.0f, (_Float16)8.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = codes(raw, parity2, i);
+            const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
+            out[2 * i + 0] = as_u32((code_pair<false>(n) - off) * d);
+            out[2 * i + 1] = as_u32((code_pair<true>(n) - off) * d);
+        }
+    }
+    __device__ static bool needs_exact(const uint32_t raw[5], uint32_t parity2) {
+        return !(__builtin_fabsf(h2f(scale_bits(raw, parity2))) <= kQ4_0FastMaxScale);
+    }
+    __device__ static void decode_half(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
+        decode_half_exact(raw, parity2, h, out);
     }
     __device__ static uint32_t parity(uint32_t col_off, uint32_t kb) { return (col_off + kb * 18u) & 2u; }
 };
@@ -77,8 +109,8 @@ template <> struct Decoder<QUANT_MLX_4BIT> {
         for (int i = 0; i < 4; i++) {
             const uint32_t q = raw[i + 1];
             const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
-            out[2 * i + 0] = as_u32(__builtin_elementwise_fma(magic_to_q(nib_pair_lo(n)), d, bias));
-            out[2 * i + 1] = as_u32(__builtin_elementwise_fma(magic_to_q(nib_pair_hi(n)), d, bias));
+            out[2 * i + 0] = as_u32(__builtin_elementwise_fma(code_pair<false>(n), d, bias));
+            out[2 * i + 1] = as_u32(__builtin_elementwise_fma(code_pair<true>(n), d, bias));
         }
     }
     __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
@@ -129,8 +161,8 @@ template <> struct Decoder<QUANT_Q4_K> {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t n = (h ? (raw[4 + i] >> 4) : raw[4 + i]) & 0x0f0f0f0fu;
-            out[2 * i + 0] = affine_pair_exact(nib_pair_lo(n), A, -B);
-            out[2 * i + 1] = affine_pair_exact(nib_pair_hi(n), A, -B);
+            out[2 * i + 0] = affine_pair_exact(code_pair<false>(n), A, -B);
+            out[2 * i + 1] = affine_pair_exact(code_pair<true>(n), A, -B);
         }
     }
     __device__ static bool needs_exact(const uint32_t raw[8], uint32_t s) {
@@ -147,15 +179,15 @@ template <> struct Decoder<QUANT_Q4_K> {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t n = (h ? (raw[4 + i] >> 4) : raw[4 + i]) & 0x0f0f0f0fu;
-                out[2 * i + 0] = affine_pair_exact(nib_pair_lo(n), A, -B);
-                out[2 * i + 1] = affine_pair_exact(nib_pair_hi(n), A, -B);
+                out[2 * i + 0] = affine_pair_exact(code_pair<false>(n), A, -B);
+                out[2 * i + 1] = affine_pair_exact(code_pair<true>(n), A, -B);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t n = (h ? (raw[4 + i] >> 4) : raw[4 + i]) & 0x0f0f0f0fu;
-                out[2 * i + 0] = affine_pair_any(nib_pair_lo(n), A, -B, fast);
-                out[2 * i + 1] = affine_pair_any(nib_pair_hi(n), A, -B, fast);
+                out[2 * i + 0] = affine_pair_any(code_pair<false>(n), A, -B, fast);
+                out[2 * i + 1] = affine_pair_any(code_pair<true>(n), A, -B, fast);
             }
         }
     }
@@ -199,16 +231,16 @@ template <> struct Decoder<QUANT_TERNARY_1_58> {
 };
 
 // Branch-free half-group decode for pipelined callers: bit-exact whenever no
-// lane of the wave has needs_exact() true for its group (only Q4_K has a slow
-// path; its callers check and re-decode with decode_group otherwise).
+// lane of the wave has needs_exact() true for its group (Q4_K and Q4_0 have a
+// slow path; callers check and re-decode with decode_group otherwise).
 template <int F>
 __device__ __forceinline__ void decode_half_fast(const uint32_t* raw, uint32_t parity, int h, uint32_t out[8]) {
-    if constexpr (F == QUANT_Q4_K) Decoder<F>::decode_half_fast(raw, parity, h, out);
+    if constexpr (F == QUANT_Q4_K || F == QUANT_Q4_0) Decoder<F>::decode_half_fast(raw, parity, h, out);
     else Decoder<F>::decode_half(raw, parity, h, out);
 }
 template <int F>
 __device__ __forceinline__ bool needs_exact(const uint32_t* raw, uint32_t parity) {
-    if constexpr (F == QUANT_Q4_K) return Decoder<F>::needs_exact(raw, parity);
+    if constexpr (F == QUANT_Q4_K || F == QUANT_Q4_0) return Decoder<F>::needs_exact(raw, parity);
     else return false;
 }
 

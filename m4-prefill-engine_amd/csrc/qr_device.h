@@ -82,19 +82,30 @@ __device__ __forceinline__ h2_t magic_to_q(uint32_t magic_pair) {
     return as_h2(magic_pair) - off;
 }
 
-// RNE binary16 of q*A + C for both codes of a magic pair, when q*A + C is
-// exact in fp32 (fused fp32 fma of the fp16 code, one rounding to fp16; maps
-// to v_fma_mix{lo,hi}_f16).
-__device__ __forceinline__ uint32_t affine_pair_exact(uint32_t magic_pair, float A, float C) {
-    const h2_t q = magic_to_q(magic_pair);
+// Exact binary16 pair {c0, c1} of two codes 0..15 held one per byte, in bytes
+// 0, 1 (HI = false) or 2, 3 (HI = true) of a word.  A byte c read as an OCP
+// e4m3 value is c * 2^-9 for every c in 0..15 (subnormal for c < 8, exponent
+// field 1 for c >= 8: the two ranges join linearly), so the scaled conversion
+// by 2^9 is exact -- one packed instruction per pair.
+template <bool HI>
+__device__ __forceinline__ h2_t code_pair(uint32_t bytes) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(bytes, 512.0f, HI);
+}
+
+// Largest |d| for which -8 d is finite in binary16 (65504 / 8).
+constexpr float kQ4_0FastMaxScale = 8188.0f;
+
+// RNE binary16 of q*A + C for both codes of a pair, when q*A + C is exact in
+// fp32 (fused fp32 fma of the fp16 code, one rounding to fp16; maps to
+// v_fma_mix{lo,hi}_f16).
+__device__ __forceinline__ uint32_t affine_pair_exact(h2_t q, float A, float C) {
     const _Float16 lo = (_Float16)__builtin_fmaf((float)q.x, A, C);
     const _Float16 hi = (_Float16)__builtin_fmaf((float)q.y, A, C);
     return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
 }
 
 // Same for any inputs: the exact-sum (round-to-odd) path where `exact` is false.
-__device__ __forceinline__ uint32_t affine_pair_any(uint32_t magic_pair, float A, float C, bool exact) {
-    const h2_t q = magic_to_q(magic_pair);
+__device__ __forceinline__ uint32_t affine_pair_any(h2_t q, float A, float C, bool exact) {
     const float q0 = (float)q.x, q1 = (float)q.y;
     const uint32_t lo = exact ? f2h_bits(__builtin_fmaf(q0, A, C)) : rne16_sum(q0 * A, C);
     const uint32_t hi = exact ? f2h_bits(__builtin_fmaf(q1, A, C)) : rne16_sum(q1 * A, C);

@@ -65,9 +65,19 @@ template <> struct Frag<QUANT_Q4_0> {
         q0 &= 0x0f0f0f0fu;
         q1 &= 0x0f0f0f0fu;
         const h2_t d = as_h2(d16 | (d16 << 16));
-        const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-        u4_t w = {as_u32((as_h2(nib_pair_lo(q0)) - off) * d), as_u32((as_h2(nib_pair_hi(q0)) - off) * d),
-                  as_u32((as_h2(nib_pair_lo(q1)) - off) * d), as_u32((as_h2(nib_pair_hi(q1)) - off) * d)};
+        u4_t w;
+        if (__all(__builtin_fabsf(h2f(d16)) <= kQ4_0FastMaxScale)) {  // fma(q, d, -8d): -8d exact
+            const h2_t m8 = {(_Float16)-8.0f, (_Float16)-8.0f};
+            const h2_t c = d * m8;
+            w = u4_t{as_u32(__builtin_elementwise_fma(code_pair<false>(q0), d, c)),
+                     as_u32(__builtin_elementwise_fma(code_pair<true>(q0), d, c)),
+                     as_u32(__builtin_elementwise_fma(code_pair<false>(q1), d, c)),
+                     as_u32(__builtin_elementwise_fma(code_pair<true>(q1), d, c))};
+        } else {  // (q - 8) * d
+            const h2_t off = {(_Float16)8.0f, (_Float16)8.0f};
+            w = u4_t{as_u32((code_pair<false>(q0) - off) * d), as_u32((code_pair<true>(q0) - off) * d),
+                     as_u32((code_pair<false>(q1) - off) * d), as_u32((code_pair<true>(q1) - off) * d)};
+        }
         return __builtin_bit_cast(h8_t, w);
     }
 };
@@ -92,11 +102,10 @@ template <> struct Frag<QUANT_MLX_4BIT> {
         q1 &= 0x0f0f0f0fu;
         const uint32_t d16 = db & 0xffffu, b16 = db >> 16;
         const h2_t d = as_h2(d16 | (d16 << 16)), bias = as_h2(b16 | (b16 << 16));
-        const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
-        u4_t w = {as_u32(__builtin_elementwise_fma(as_h2(nib_pair_lo(q0)) - off, d, bias)),
-                  as_u32(__builtin_elementwise_fma(as_h2(nib_pair_hi(q0)) - off, d, bias)),
-                  as_u32(__builtin_elementwise_fma(as_h2(nib_pair_lo(q1)) - off, d, bias)),
-                  as_u32(__builtin_elementwise_fma(as_h2(nib_pair_hi(q1)) - off, d, bias))};
+        u4_t w = {as_u32(__builtin_elementwise_fma(code_pair<false>(q0), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<true>(q0), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<false>(q1), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<true>(q1), d, bias))};
         return __builtin_bit_cast(h8_t, w);
     }
 };
@@ -133,11 +142,11 @@ template <> struct Frag<QUANT_Q4_K> {
         q1 &= 0x0f0f0f0fu;
         u4_t w;
         if (__all(fast)) {  // exact-sum path only when some lane needs it
-            w = u4_t{affine_pair_exact(nib_pair_lo(q0), A, -B), affine_pair_exact(nib_pair_hi(q0), A, -B),
-                     affine_pair_exact(nib_pair_lo(q1), A, -B), affine_pair_exact(nib_pair_hi(q1), A, -B)};
+            w = u4_t{affine_pair_exact(code_pair<false>(q0), A, -B), affine_pair_exact(code_pair<true>(q0), A, -B),
+                     affine_pair_exact(code_pair<false>(q1), A, -B), affine_pair_exact(code_pair<true>(q1), A, -B)};
         } else {
-            w = u4_t{affine_pair_any(nib_pair_lo(q0), A, -B, fast), affine_pair_any(nib_pair_hi(q0), A, -B, fast),
-                     affine_pair_any(nib_pair_lo(q1), A, -B, fast), affine_pair_any(nib_pair_hi(q1), A, -B, fast)};
+            w = u4_t{affine_pair_any(code_pair<false>(q0), A, -B, fast), affine_pair_any(code_pair<true>(q0), A, -B, fast),
+                     affine_pair_any(code_pair<false>(q1), A, -B, fast), affine_pair_any(code_pair<true>(q1), A, -B, fast)};
         }
         return __builtin_bit_cast(h8_t, w);
     }
