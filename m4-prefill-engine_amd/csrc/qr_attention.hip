@@ -75,44 +75,167 @@ hipError_t launch_quantize_q8_0(const _Float16* src, uint8_t* dst, size_t nblock
 constexpr int kBQ = 128;      // queries per workgroup
 constexpr int kBKV = 64;      // keys per tile
 
-// Dequantize one Q8_0 block (34 bytes at byte offset o of the rsrc) into 16
-// half2 words: w[p] = {q[2p] * d, q[2p+1] * d}, each rounded once.
-__device__ __forceinline__ void q8_block_to_h2(__amdgpu_buffer_rsrc_t r, uint32_t o, uint32_t out[16]) {
-    const uint32_t a = o & ~3u;
-    uint32_t raw[10];
-#pragma unroll
-    for (int i = 0; i < 9; i++) raw[i] = ld_b32(r, a + 4u * i);
-    raw[9] = 0;
-    const bool par = (o & 2u) != 0;
-    const uint32_t d16 = par ? (raw[0] >> 16) : (raw[0] & 0xffffu);
-    uint32_t q[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = par ? raw[i + 1] : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
-    const h2_t d = as_h2(d16 | (d16 << 16));
+// Two Q8_0 codes of bytes 0, 1 (HI = false) or 2, 3 (HI = true) of a code word
+// times d: the code plus 128 becomes the binary16 1024 + 128 + q through the
+// magic exponent (exact), 1152 is subtracted (exact) and the product rounds
+// once -- the reference's half(q * d) (brick4_attn_bench.mm:57-65).
+template <bool HI>
+__device__ __forceinline__ uint32_t q8_pair(uint32_t codes, h2_t d) {
     const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t u = codes ^ 0x80808080u;  // two's complement byte -> q + 128
+    return as_u32((as_h2(HI ? nib_pair_hi(u) : nib_pair_lo(u)) - off) * d);
+}
+
+// Tile staging.  Per 64-key tile, one "unit" per thread and pass:
+//  K unit  = one Q8_0 block (key, 32 dims) -> 32 halfs of row `key` of Ks;
+//  V unit  = 16 dims of two adjacent keys  -> 16 half2 {V[k][d], V[k+1][d]}
+//            written to rows d of the transposed tile Vt[d][key].
+// Raw words are fetched one tile ahead of the decode (two register sets).
+template <int D>
+struct AttnStage {
+    static constexpr int NB = D / 32;                 // Q8_0 blocks per key
+    static constexpr int KU = kBKV * NB;              // K units per tile
+    static constexpr int VU = (kBKV / 2) * (D / 16);  // V units per tile
+    static constexpr int UPT = (KU + VU) / 256;       // units per thread
+    static_assert((KU + VU) % 256 == 0 && KU % 64 == 0, "whole passes; each wave stages only K or only V");
+};
+
+// Raw words of one thread's units: K units use k (9 words: the block's dwords),
+// V units v (two keys x {scale dword, 5 code dwords}).  Separate arrays, so the
+// two unit kinds never share a register slot.
+template <int D>
+struct AttnRaw {
+    uint32_t k[AttnStage<D>::UPT][9];
+    uint32_t v[AttnStage<D>::UPT][12];
+};
+
+template <int D>
+__device__ __forceinline__ void attn_fetch(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int k0, int M, int tid,
+                                           AttnRaw<D>& raw) {
+    using S = AttnStage<D>;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        uint32_t u = q[i] ^ 0x80808080u;  // two's complement byte -> q + 128
-        out[2 * i] = as_u32((as_h2(nib_pair_lo(u)) - off) * d);
-        out[2 * i + 1] = as_u32((as_h2(nib_pair_hi(u)) - off) * d);
+    for (int i = 0; i < S::UPT; i++) {
+        const int u = tid + 256 * i;
+        if (__builtin_amdgcn_readfirstlane(u) < S::KU) {  // wave-uniform: K units fill whole waves
+            const int key = u % kBKV, db = u / kBKV;
+            const int gk = k0 + key;
+            const uint32_t o = gk < M ? (uint32_t)(gk * S::NB + db) * 34u : kOOB;
+            const uint32_t a = o & ~3u;
+#pragma unroll
+            for (int w = 0; w < 9; w++) raw.k[i][w] = ld_b32(kr, a + 4u * w);
+            asm volatile("; staged K fetch" ::: "memory");  // keeps the branches' stores apart (SROA)
+        } else {
+            const int v = u - S::KU;
+            const int kp = v % (kBKV / 2), dg = v / (kBKV / 2);  // key pair, 16-dim group
+            const int db = dg >> 1, hh = dg & 1;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int gk = k0 + 2 * kp + e;
+                const uint32_t o = gk < M ? (uint32_t)(gk * S::NB + db) * 34u : kOOB;
+                const uint32_t cs = o + 2u + 16u * (uint32_t)hh;  // first code byte
+                const uint32_t a = cs & ~3u;
+                raw.v[i][6 * e] = ld_b32(vr, o & ~3u);             // holds d
+#pragma unroll
+                for (int w = 0; w < 5; w++) raw.v[i][6 * e + 1 + w] = ld_b32(vr, a + 4u * w);
+            }
+            asm volatile("; staged V fetch" ::: "memory");
+        }
     }
 }
 
 template <int D>
-__global__ void __launch_bounds__(256) flash_attn_q8_0_kernel(AttnParams p) {
-    constexpr int NB = D / 32;                 // Q8_0 blocks per token row
+__device__ __forceinline__ void attn_stage(const AttnRaw<D>& raw, int k0, int tid,
+                                           _Float16* Ks, _Float16* Vt) {
+    using S = AttnStage<D>;
+    constexpr int KROW = D + 8, VROW = kBKV + 8;
+#pragma unroll
+    for (int i = 0; i < S::UPT; i++) {
+        const int u = tid + 256 * i;
+        if (__builtin_amdgcn_readfirstlane(u) < S::KU) {
+            const int key = u % kBKV, db = u / kBKV;
+            const uint32_t o = (uint32_t)((k0 + key) * S::NB + db) * 34u;
+            const bool par = (o & 2u) != 0;
+            const uint32_t d16 = par ? (raw.k[i][0] >> 16) : (raw.k[i][0] & 0xffffu);
+            const h2_t d = as_h2(d16 | (d16 << 16));
+            uint32_t w[16];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const uint32_t q = par ? raw.k[i][c + 1] : __builtin_amdgcn_alignbyte(raw.k[i][c + 1], raw.k[i][c], 2);
+                w[2 * c] = q8_pair<false>(q, d);
+                w[2 * c + 1] = q8_pair<true>(q, d);
+            }
+            u4_t* dst = reinterpret_cast<u4_t*>(Ks + key * KROW + db * 32);
+#pragma unroll
+            for (int c = 0; c < 4; c++) dst[c] = u4_t{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+        } else {
+            const int v = u - S::KU;
+            const int kp = v % (kBKV / 2), dg = v / (kBKV / 2);
+            const int db = dg >> 1, hh = dg & 1;
+            uint32_t w[2][8];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t o = (uint32_t)((k0 + 2 * kp + e) * S::NB + db) * 34u;
+                const uint32_t sh = (o + 2u) & 3u;  // code bytes start 0 or 2 bytes into the first word
+                const uint32_t d16 = (o & 2u) ? (raw.v[i][6 * e] >> 16) : (raw.v[i][6 * e] & 0xffffu);
+                const h2_t d = as_h2(d16 | (d16 << 16));
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t q = __builtin_amdgcn_alignbyte(raw.v[i][6 * e + 2 + c], raw.v[i][6 * e + 1 + c], sh);
+                    w[e][2 * c] = q8_pair<false>(q, d);
+                    w[e][2 * c + 1] = q8_pair<true>(q, d);
+                }
+            }
+            // w[e][c] = {V[key e][16dg + 2c], V[key e][16dg + 2c + 1]}
+            uint32_t* vt = reinterpret_cast<uint32_t*>(Vt);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int dd = 16 * dg + 2 * c;
+                vt[(dd * VROW + 2 * kp) >> 1] = perm(w[1][c], w[0][c], 0x05040100u);
+                vt[((dd + 1) * VROW + 2 * kp) >> 1] = perm(w[1][c], w[0][c], 0x07060302u);
+            }
+        }
+    }
+}
+
+// Flash attention over a Q8_0 K/V cache (one workgroup = 4 wave64s = 128
+// queries of one head).
+//  * Each wave owns 32 queries and computes S^T = K . Q^T with
+//    v_mfma_f32_32x32x16_f16, so a lane owns ONE query column: softmax row
+//    statistics are lane-local over its accumulator rows plus one exchange
+//    with the partner lane (l ^ 32).
+//  * K/V tiles of 64 keys are dequantized once per workgroup from Q8_0 into a
+//    double-buffered LDS stage (K as [key][d], V transposed as [d][key]); the
+//    raw blocks of tile t + 1 are fetched while tile t is multiplied, and
+//    decoded after it, so one barrier per tile and no exposed fetch latency.
+//  * Softmax in log2 units with the scale folded into one fma per score; the
+//    causal mask is applied only on tiles that cross the wave's diagonal; the
+//    running output is rescaled only when some lane's maximum moved.
+//  * P stays in registers: the S^T accumulator of a lane already holds the
+//    8 keys that lane supplies as the B operand of O^T = V^T . P^T.
+//  * fp32 running max / sum / output accumulators (the reference keeps S, P
+//    and O in half); the output is rounded to fp16 once.
+template <int D>
+__global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(AttnParams p) {
+    using S = AttnStage<D>;
     constexpr int KROW = D + 8;                // LDS row (halfs) of K tile [key][d]
     constexpr int VROW = kBKV + 8;             // LDS row (halfs) of V^T tile [d][key]
     constexpr int DT = D / 32;                 // 32-row output tiles along d
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[kBKV * KROW];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VROW];
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kBKV * KROW];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VROW];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, j = lane & 31;
-    const uint32_t M = p.M;
-    const int qtiles = (int)((M + kBQ - 1) / kBQ);
-    const int qt = qtiles - 1 - (int)blockIdx.x;   // heaviest (latest) tiles first
-    const int h = blockIdx.y;
+    const int M = (int)p.M;
+    const int qtiles = (M + kBQ - 1) / kBQ;
+    // Work of a query tile grows with its index (causal).  Rank r orders the
+    // (tile, head) pairs heaviest first; workgroup b of the first half takes
+    // rank b and workgroup b + half rank total - 1 - b, so the two workgroups a
+    // CU receives in dispatch order sum to about the same work everywhere.
+    const int total = qtiles * (int)p.H, half = (total + 1) / 2;
+    const int b = (int)blockIdx.x;
+    const int rank = b < half ? b : total - 1 - (b - half);
+    const int qt = qtiles - 1 - rank / (int)p.H;
+    const int h = rank % (int)p.H;
     const int q0 = qt * kBQ;
     const int qw = q0 + wave * 32;                 // this wave's first query
     const int my_q = qw + j;                       // this lane's query
@@ -123,55 +246,46 @@ __global__ void __launch_bounds__(256) flash_attn_q8_0_kernel(AttnParams p) {
     auto kr = make_rsrc(p.Kq + (size_t)h * (head_elems / 32) * 34, kv_bytes);
     auto vr = make_rsrc(p.Vq + (size_t)h * (head_elems / 32) * 34, kv_bytes);
 
+    const int q_last = min(q0 + kBQ, M) - 1;
+    const int ntiles = q_last / kBKV + 1;
+
+    // ---- prologue: tile 0 staged, tile 1 in flight ----
+    AttnRaw<D> rawA, rawB;
+    attn_fetch<D>(kr, vr, 0, M, tid, rawA);
+    if (ntiles > 1) attn_fetch<D>(kr, vr, kBKV, M, tid, rawB);
+
     // Q^T fragments (B operand): lane holds Q[my_q][kk*16 + 8g .. +7].
     h8_t qf[D / 16];
     {
         auto qr_ = make_rsrc(Qh, (uint32_t)(head_elems * 2));
 #pragma unroll
         for (int kk = 0; kk < D / 16; kk++) {
-            uint32_t off = my_q < (int)M ? ((uint32_t)my_q * D + kk * 16 + 8 * g) * 2u : kOOB;
+            uint32_t off = my_q < M ? ((uint32_t)my_q * D + kk * 16 + 8 * g) * 2u : kOOB;
             u4_t v = ld_b128(qr_, off);
             qf[kk] = __builtin_bit_cast(h8_t, v);
         }
     }
+    attn_stage<D>(rawA, 0, tid, Ks[0], Vt[0]);
+    __syncthreads();
 
-    const float sl2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+    // scores -> log2 units: s * c with c > 0 (a negative scale flips the sign
+    // of Q once, exactly, so the running maximum stays a maximum of s)
+    float c = p.scale * 1.4426950408889634f;
+    if (c < 0.0f) {
+        c = -c;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; kk++) qf[kk] = -qf[kk];
+    }
     float m_run = -INFINITY, l_run = 0.0f;
     f16v_t o[DT];
 #pragma unroll
     for (int t = 0; t < DT; t++) o[t] = f16v_t{};
 
-    const int q_last = min(q0 + kBQ, (int)M) - 1;
-    const int ntiles = q_last / kBKV + 1;
-
-    for (int kt = 0; kt < ntiles; kt++) {
+    auto compute = [&](int kt) {
         const int k0 = kt * kBKV;
-        __syncthreads();  // previous tile fully consumed
-        // ---- dequantize K and V tiles into LDS: 2 * 64 * NB blocks ----
-        for (int bi = tid; bi < 2 * kBKV * NB; bi += 256) {
-            const bool isv = bi >= kBKV * NB;
-            const int b = isv ? bi - kBKV * NB : bi;
-            const int key = b % kBKV, db = b / kBKV;   // adjacent lanes: adjacent keys
-            const int gk = k0 + key;
-            uint32_t off = gk < (int)M ? (uint32_t)(gk * NB + db) * 34u : kOOB;
-            uint32_t w[16];
-            q8_block_to_h2(isv ? vr : kr, off, w);
-            if (!isv) {
-                u4_t* dst = reinterpret_cast<u4_t*>(Ks + key * KROW + db * 32);
-#pragma unroll
-                for (int i = 0; i < 4; i++) dst[i] = u4_t{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
-            } else {
-                uint16_t* vt = reinterpret_cast<uint16_t*>(Vt);
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    vt[(db * 32 + 2 * i) * VROW + key] = (uint16_t)(w[i] & 0xffffu);
-                    vt[(db * 32 + 2 * i + 1) * VROW + key] = (uint16_t)(w[i] >> 16);
-                }
-            }
-        }
-        __syncthreads();
-        if (k0 > qw + 31) continue;  // whole tile above this wave's diagonal
-
+        if (k0 > qw + 31) return;  // whole tile above this wave's diagonal
+        const _Float16* Kb = Ks[kt & 1];
+        const _Float16* Vb = Vt[kt & 1];
         // ---- S^T = K . Q^T : two 32-key tiles ----
         f16v_t s[2];
 #pragma unroll
@@ -179,24 +293,27 @@ __global__ void __launch_bounds__(256) flash_attn_q8_0_kernel(AttnParams p) {
             s[ks] = f16v_t{};
 #pragma unroll
             for (int kk = 0; kk < D / 16; kk++) {
-                h8_t a = *reinterpret_cast<const h8_t*>(Ks + (ks * 32 + j) * KROW + kk * 16 + 8 * g);
+                h8_t a = *reinterpret_cast<const h8_t*>(Kb + (ks * 32 + j) * KROW + kk * 16 + 8 * g);
                 s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[ks], 0, 0, 0);
             }
         }
-        // ---- mask, scale, running max ----
+        // ---- causal mask (diagonal tiles only), running max ----
+        if (k0 + kBKV - 1 > qw) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = k0 + ks * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    s[ks][r] = (key <= my_q && key < M) ? s[ks][r] : -INFINITY;
+                }
+        }
         float tmax = -INFINITY;
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = k0 + ks * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                float v = s[ks][r] * sl2;
-                v = (key <= my_q && key < (int)M) ? v : -INFINITY;
-                s[ks][r] = v;
-                tmax = fmaxf(tmax, v);
-            }
+            for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s[ks][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
+        const float m_new = fmaxf(m_run, tmax * c);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
         m_run = m_new;
         float lsum = 0.0f;
@@ -205,16 +322,18 @@ __global__ void __launch_bounds__(256) flash_attn_q8_0_kernel(AttnParams p) {
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
-                float e0 = __builtin_amdgcn_exp2f(s[ks][r] - m_new);
-                float e1 = __builtin_amdgcn_exp2f(s[ks][r + 1] - m_new);
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][r], c, -m_new));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][r + 1], c, -m_new));
                 lsum += e0 + e1;
                 pk[ks][r >> 1] = pack_h2(f2h_bits(e0), f2h_bits(e1));
             }
         l_run = l_run * alpha + lsum;
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int t = 0; t < DT; t++)
+            for (int t = 0; t < DT; t++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+                for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+        }
 
         // ---- O^T += V^T . P^T : 4 k16 steps over the 64 keys ----
         // step (ks, t2): B operand = P rows r = 8*t2 .. 8*t2+7 of tile ks, i.e. keys
@@ -228,19 +347,33 @@ __global__ void __launch_bounds__(256) flash_attn_q8_0_kernel(AttnParams p) {
                 const int kb0 = ks * 32 + t2 * 16 + 4 * g;
 #pragma unroll
                 for (int t = 0; t < DT; t++) {
-                    const _Float16* row = Vt + (t * 32 + j) * VROW;
+                    const _Float16* row = Vb + (t * 32 + j) * VROW;
                     u2_t lo = *reinterpret_cast<const u2_t*>(row + kb0);
                     u2_t hi = *reinterpret_cast<const u2_t*>(row + kb0 + 8);
                     u4_t aw = {lo.x, lo.y, hi.x, hi.y};
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, aw), b, o[t], 0, 0, 0);
                 }
             }
+    };
+
+    // ---- main loop, unrolled by two for the raw register sets:
+    // iteration kt: fetch tile kt + 2, multiply tile kt, stage tile kt + 1 ----
+    for (int kt = 0; kt < ntiles; kt += 2) {
+        if (kt + 2 < ntiles) attn_fetch<D>(kr, vr, (kt + 2) * kBKV, M, tid, rawA);
+        compute(kt);
+        if (kt + 1 < ntiles) attn_stage<D>(rawB, (kt + 1) * kBKV, tid, Ks[(kt + 1) & 1], Vt[(kt + 1) & 1]);
+        __syncthreads();
+        if (kt + 1 >= ntiles) break;
+        if (kt + 3 < ntiles) attn_fetch<D>(kr, vr, (kt + 3) * kBKV, M, tid, rawB);
+        compute(kt + 1);
+        if (kt + 2 < ntiles) attn_stage<D>(rawA, (kt + 2) * kBKV, tid, Ks[kt & 1], Vt[kt & 1]);
+        __syncthreads();
     }
 
     // ---- normalize and store ----
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (my_q < (int)M) {
+    if (my_q < M) {
 #pragma unroll
         for (int t = 0; t < DT; t++)
 #pragma unroll
@@ -255,7 +388,7 @@ __global__ void __launch_bounds__(256) flash_attn_q8_0_kernel(AttnParams p) {
 }
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
-    dim3 grid((p.M + kBQ - 1) / kBQ, p.H);
+    dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
     switch (p.D) {
         case 64: hipLaunchKernelGGL(flash_attn_q8_0_kernel<64>, grid, dim3(256), 0, st, p); break;
         case 128: hipLaunchKernelGGL(flash_attn_q8_0_kernel<128>, grid, dim3(256), 0, st, p); break;

@@ -267,6 +267,32 @@ def test_flash_attention_q8_0(bridge, oracle, D, M):
     assert torch.isfinite(O).all()
 
 
+@pytest.mark.parametrize("D,M", [(64, 1000), (128, 777)])
+def test_flash_attention_many_tiles(bridge, oracle, D, M):
+    """Many 64-key tiles per query block: the pipelined K/V staging (fetch one
+    tile ahead, two LDS buffers) across both unrolled halves and odd counts."""
+    H = 2
+    rng = np.random.default_rng(D + M)
+    Q, K, V = (rng.standard_normal((H, M, D)).astype(np.float16) for _ in range(3))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    O = empty16(H, M, D)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), O, H, M, D, scale)
+    bridge.synchronize()
+    assert maxdiff(host(O), oracle.attention_q8_0(Q, Kq, Vq, scale)) <= TOL
+
+
+def test_flash_attention_negative_scale(bridge, oracle):
+    H, M, D = 2, 200, 64
+    rng = np.random.default_rng(17)
+    Q, K, V = ((rng.standard_normal((H, M, D)) * 0.5).astype(np.float16) for _ in range(3))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    O = empty16(H, M, D)
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), O, H, M, D, -0.125)
+    bridge.synchronize()
+    assert maxdiff(host(O), oracle.attention_q8_0(Q, Kq, Vq, -0.125)) <= TOL
+
+
 def test_flash_attention_unit_scale_inputs(bridge, oracle):
     """N(0,1) activations (BASELINE config 5 scale): larger logits."""
     H, M, D = 4, 300, 64
