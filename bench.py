@@ -355,7 +355,7 @@ def main():
                    "M": 128, "K": 4096, "N": 14336, "format": "MLX_4BIT (g64 repacked to 32-blocks)"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "gemm_kernel<QUANT_MLX_4BIT>", "hbm_frac": head.get("frac_hbm")},
+                     "kernel": "gemm_rb_kernel<MLX_4BIT, 4, 1, 4> (128x128 tiles, K split 2)", "hbm_frac": head.get("frac_hbm")},
         "per_config": per,
     }
     if not a.no_cpu_baseline and head_inputs is not None:

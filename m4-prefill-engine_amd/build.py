@@ -17,7 +17,7 @@ OUT = HERE / "libm4_bridge.so"
 BUILD = HERE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["qr_gemm.hip", "qr_gemm_rb.hip", "qr_gemm_skinny.hip", "qr_dequant.hip", "qr_attention.hip", "qr_bridge.cpp", "qr_registry.cpp"]
+SOURCES = ["qr_gemm.hip", "qr_gemm_skinny.hip", "qr_dequant.hip", "qr_attention.hip", "qr_bridge.cpp", "qr_registry.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-ffp-contract=on",
           "-fvisibility=hidden", "-Wall", "-Wno-unused-function", "-Wno-unused-variable",

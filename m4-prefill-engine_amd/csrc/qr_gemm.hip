@@ -1,69 +1,80 @@
-// qr_gemm.hip -- quantized projection Y = X . W^T on gfx950 MFMA (tiled, M > 64).
+// qr_gemm.hip -- quantized projection Y = X . W^T on gfx950 MFMA, weights
+// decoded straight into MFMA B-operand registers (tiled, M > 64).
 //
 // Replaces the reference's block_mma_64x64_engine (quant_router_kernels.metal:
-// 442-581) and its 14 entry points (:588-927), and the fused dual-projection
+// 442-581) with its entry points (:588-927), and the fused dual-projection
 // SwiGLU swiglu_mma_dual_simd (brick3_swiglu_kernels.metal:428-698).
 //
-// Design (one workgroup = 4 or 8 wave64s, one BM x BN output tile, the K range
-// split across `ksplit` workgroups when the tile grid alone cannot fill the GPU):
-//  * K advances 64 per step (two 32-element weight groups per column).
-//  * The X tile [BM x 64] fp16 is fetched with 16-byte buffer loads; the
-//    weight groups of the BN columns are fetched raw (compressed) and decoded
-//    in registers to binary16 (qr_decode.h, bit-exact vs the CPU unpack), a
-//    half group (16 elements) per thread when the workgroup has enough threads.
-//    Fetches run P steps ahead of the MFMAs (P register stages), so HBM/L2
-//    latency hides behind P-1 steps of matrix work.
-//  * Decoded tiles go to a double-buffered LDS stage (one barrier per step).
-//    Both operands are K-contiguous, so each lane fetches its 8 halfs of a
-//    v_mfma_f32_32x32x16_f16 operand with one ds_read_b128; rows are padded
-//    by 8 halfs to spread the LDS banks.  With 8 waves, two waves share each
-//    SIMD, so one wave's decode VALU work overlaps the other's MFMAs.
-//  * Tiles are assigned XCD-aware: consecutive workgroup ids land on
-//    different XCDs, so ids are remapped to give each XCD a contiguous run of
-//    tiles grouped 2 row-tiles x many column-tiles (shared L2 reuse of X
-//    rows and weight columns).
+// One workgroup = NW wave64s and one BM x BN output tile (BM = 32 TM rows,
+// BN = NW x 32 TN columns).  The waves split the tile along N only, so every
+// weight column belongs to exactly one wave and is decoded exactly once per
+// workgroup:
+//  * K advances 64 per step = two 32-element quant groups per column.  For
+//    v_mfma_f32_32x32x16_f16 lane l supplies column l % 32 and the 8 k values
+//    8 (l / 32) .. +7 of each 16-wide slice; here the K order inside a step is
+//    permuted so that lane half h = l / 32 owns quant group h of the step
+//    whole: at slice kk the lane holds elements 8 kk .. 8 kk + 7 of its group.
+//    The sum over k is order-free, so X (the A operand) is read with the same
+//    permutation: row r, k = 32 h + 8 kk + i.
+//  * Each lane fetches the raw block of its (column, group) with buffer loads
+//    P steps ahead and decodes all 32 weights to binary16 in registers
+//    (qr_decode.h: bit-exact vs the CPU unpack).  No LDS traffic for weights.
+//  * The X tile [BM x 64] fp16 is fetched with 16-byte buffer loads (P steps
+//    ahead) into a double-buffered LDS stage, padded 8 halfs per row so the
+//    ds_read_b128 fragment reads are bank-conflict free; one barrier per step.
+//    Per step a wave reads BM x 64 x 2 bytes of LDS for BM x 32 TN x 64 x 2
+//    flop: with TN = 2 that is half the LDS bandwidth at full MFMA rate.
+//  * The MFMAs of step s, the decode of step s + 1 and the fetches of step
+//    s + 1 + P sit in one basic block (the main loop is unrolled by P and
+//    branch-free), so decode VALU work issues under the matrix pipe.
+//  * XCD-aware tile order (consecutive workgroup ids land on different XCDs):
+//    each XCD gets a contiguous run of tiles, grouped GM row-tiles x many
+//    column-tiles so X rows and weight columns are reused from its L2.
 //  * Epilogue: fp32 accumulators (+ fp16 residual, + SwiGLU for the dual
-//    variant) rounded once to fp16, written [M, N] or head-major [H, M, D]
-//    (quant_router_kernels.metal:570-574).  With a K split, the partial
-//    accumulators go to a workspace with agent-scope stores and the last
-//    workgroup of the tile (agent-scope counter) sums them in split order --
-//    deterministic, one launch.
+//    variant) rounded once to fp16, staged through LDS for 16-byte stores,
+//    written [M, N] or head-major [H, M, D] (quant_router_kernels.metal:570-574).
+//    K split across workgroups: partials go to a workspace with agent-scope
+//    stores; the last workgroup of the tile (agent-scope counter) sums them in
+//    split order -- deterministic, one launch.
 #include "qr_decode.h"
 #include "qr_kernels.h"
 
-#include <stdlib.h>
-
 namespace qr {
 
-constexpr int kBK = 64;
-constexpr int kLdsRow = kBK + 8;  // halfs per LDS row (padding vs bank conflicts)
+#ifndef QR_RB_STAGES
+#define QR_RB_STAGES 2
+#endif
+#ifndef QR_RB_VPM
+#define QR_RB_VPM 5
+#endif
 
-template <int F, int WGM, int WGN, int TM, int TN, bool DUAL>
-struct GemmCfg {
-    static constexpr int NT = 64 * WGM * WGN;             // threads
-    static constexpr int BM = WGM * TM * 32;
-    static constexpr int BN = WGN * TN * 32;
-    static constexpr int NCOL = DUAL ? 2 * BN : BN;       // weight columns decoded per step
-    static constexpr int HALVES = NCOL * 4;               // 16-element half groups per step
-    static constexpr bool HALF = NT >= HALVES;            // one half group per thread
-    static constexpr int UNITS = HALF ? HALVES : NCOL * 2;
-    static constexpr int UPT = (UNITS + NT - 1) / NT;     // decode units per thread
-    static constexpr int XCH = BM * kBK / 8;              // 16-byte X chunks per step
+
+namespace rb {
+
+constexpr int kBK = 64;
+constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
+
+template <int TM, int TN, int NW, bool DUAL>
+struct Cfg {
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 32 * TM;
+    static constexpr int WN = 32 * TN;            // columns per wave
+    static constexpr int BN = NW * WN;
+    static constexpr int NCB = DUAL ? 2 * TN : TN;  // 32-column B tiles per wave (gate, then up)
+    static constexpr int XCH = BM * kBK / 8;      // 16-byte X chunks per step
     static constexpr int XPT = (XCH + NT - 1) / NT;
-    static constexpr int LDS_A = BM * kLdsRow;            // halfs per stage
-    static constexpr int LDS_B = NCOL * kLdsRow;
-    static constexpr int LDS_STAGE = LDS_A + LDS_B;
-    static constexpr int ACC = TM * TN * 16 * (DUAL ? 2 : 1);  // accumulator floats per lane
-    static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves per workgroup");
+    static constexpr int LDS_STAGE = BM * kLdsRow;  // halfs
+    static constexpr int ACC = TM * NCB * 16;     // accumulator floats per lane
+    static constexpr int EPI_BYTES = NW * 32 * (WN + 4) * 4;  // epilogue staging
+    static constexpr int LDS_BYTES = 3 * LDS_STAGE * 2 > EPI_BYTES ? 3 * LDS_STAGE * 2 : EPI_BYTES;
 };
 
-// Tile of workgroup `bid` among T tiles (nt_m x nt_n): XCD-contiguous runs,
-// grouped two row-tiles at a time.
-__device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t& tm, uint32_t& tn) {
+__device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t gm_req, uint32_t& tm,
+                                        uint32_t& tn) {
     const uint32_t T = nt_m * nt_n;
     uint32_t t = bid;
     if (T % 8 == 0) t = (bid % 8) * (T / 8) + bid / 8;
-    constexpr uint32_t GM = 2;
+    const uint32_t GM = gm_req ? gm_req : 2;
     const uint32_t per_group = GM * nt_n;
     const uint32_t grp = t / per_group;
     const uint32_t first = grp * GM;
@@ -73,30 +84,36 @@ __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt
     tn = in / gm;
 }
 
-template <int F, int WGM, int WGN, int TM, int TN, bool DUAL, int P>
-__global__ void __launch_bounds__(64 * WGM * WGN)
-gemm_kernel(GemmParams p) {
-    using C = GemmCfg<F, WGM, WGN, TM, TN, DUAL>;
+}  // namespace rb
+
+template <int F, int TM, int TN, int NW, bool DUAL, int P>
+__global__ void __launch_bounds__(64 * NW)
+gemm_rb_kernel(GemmParams p) {
+    using C = rb::Cfg<TM, TN, NW, DUAL>;
     using Dec = Decoder<F>;
     constexpr int NT = C::NT;
+    constexpr int NCB = C::NCB;
+    constexpr int kBK = rb::kBK;
+    constexpr int kLdsRow = rb::kLdsRow;
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
+    const int h = lane >> 5;     // quant group of the step this lane owns
+    const int c32 = lane & 31;
 
     const uint32_t M = p.M, N = p.N, K = p.K;
     const uint32_t nt_m = (M + C::BM - 1) / C::BM, nt_n = (N + C::BN - 1) / C::BN;
     uint32_t tmi, tni;
-    tile_of(blockIdx.x, nt_m, nt_n, tmi, tni);
+    rb::tile_of(blockIdx.x, nt_m, nt_n, p.group_m, tmi, tni);
     const int m0 = tmi * C::BM, n0 = tni * C::BN;
     const uint32_t ksplit = p.ksplit ? p.ksplit : 1;
     const uint32_t kz = blockIdx.y;
-    const uint32_t Kc = K / ksplit;                        // host guarantees divisibility
-    const uint32_t k_begin = kz * Kc;
+    const uint32_t Kc = K / ksplit;  // host guarantees divisibility (and Kc % 32 == 0)
+    const uint32_t k_begin = kz * Kc, k_end = k_begin + Kc;
     const uint32_t nsteps = (Kc + kBK - 1) / kBK;
-    const uint32_t g_begin = k_begin / 32, g_end = (k_begin + Kc) / 32;
+    const uint32_t g_begin = k_begin / 32, g_end = k_end / 32;
     const uint32_t col_bytes = (uint32_t)p.col_bytes;
 
     const int mrows = min(C::BM, (int)M - m0);
@@ -105,50 +122,46 @@ gemm_kernel(GemmParams p) {
     auto wr0 = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
     auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
 
-    uint32_t xraw[P][C::XPT][4];
-    uint32_t wraw[P][C::UPT][Dec::kRawWords];
+    // local column of B tile jb for this lane
+    auto bcol = [&](int jb) { return wave * C::WN + (jb % TN) * 32 + c32; };
 
-    // decode unit u of this thread: weight column, group within the step, half
-    auto unit_of = [&](int u, int& col, int& gsel, int& half) {
-        const int unit = tid + NT * u;
-        if (C::HALF) {
-            col = unit >> 2;
-            gsel = (unit >> 1) & 1;
-            half = unit & 1;
-        } else {
-            col = unit >> 1;
-            gsel = unit & 1;
-            half = -1;
-        }
-    };
+    // Pipelines (U = 6 steps unrolled, so every ring index below is static):
+    //  X:  raw 16-byte chunks fetched 4 steps ahead into XP = 2 register slots,
+    //      written to LDS 2 steps ahead into a 3-stage ring;
+    //  A:  fragments of slice kk + 1 read while slice kk multiplies; the first
+    //      slice of step s + 1 is read before the step's barrier (its stage was
+    //      written before the previous barrier);
+    //  W:  raw blocks fetched WP steps ahead, decoded one step ahead into the
+    //      two B buffers.
+    constexpr int XS = 3, XP = 2, WP = P, U = 6;
+    static_assert(U % XS == 0 && U % XP == 0 && U % WP == 0, "ring sizes divide the unroll");
+    uint32_t xraw[XP][C::XPT][4];
+    uint32_t wraw[WP][NCB][Dec::kRawWords];
 
-    auto load_step = [&](uint32_t step, int slot) {
+    auto load_x = [&](uint32_t step, int slot) {
         const uint32_t k0 = k_begin + step * kBK;
 #pragma unroll
         for (int i = 0; i < C::XPT; i++) {
             const int c = tid + NT * i;
             const int row = c >> 3, kc = c & 7;
-            const uint32_t k = k0 + kc * 8;
-            const uint32_t off = (c < C::XCH && k < k_begin + Kc) ? ((uint32_t)row * K + k) * 2u : kOOB;
+            const uint32_t k = k0 + kc * 8;  // past the range (or the last step): zeros
+            const uint32_t off = ((C::XCH % NT == 0 || c < C::XCH) && k < k_end) ? ((uint32_t)row * K + k) * 2u : kOOB;
             const u4_t v = ld_b128(xr, off);
             xraw[slot][i][0] = v.x; xraw[slot][i][1] = v.y; xraw[slot][i][2] = v.z; xraw[slot][i][3] = v.w;
         }
+    };
+    auto load_w = [&](uint32_t step, int slot) {
+        const uint32_t g = g_begin + step * 2 + h;
+        const bool live = g < g_end;
 #pragma unroll
-        for (int u = 0; u < C::UPT; u++) {
-            int col, gsel, half;
-            unit_of(u, col, gsel, half);
-            const uint32_t g = g_begin + step * 2 + gsel;
-            const bool up = DUAL && col >= C::BN;
-            const int lcol = up ? col - C::BN : col;
-            // out-of-range groups read as zeros (buffer bounds) and decode to zeros
-            const uint32_t coff = ((C::UNITS % NT == 0 || tid + NT * u < C::UNITS) && g < g_end) ? (uint32_t)lcol * col_bytes : kOOB;
-            Dec::load(up ? wr1 : wr0, coff, coff == kOOB ? 0u : g, wraw[slot][u]);
+        for (int jb = 0; jb < NCB; jb++) {
+            const uint32_t coff = live ? (uint32_t)bcol(jb) * col_bytes : kOOB;
+            Dec::load((DUAL && jb >= TN) ? wr1 : wr0, coff, live ? g : 0u, wraw[slot][jb]);
         }
     };
 
-    auto store_step = [&](uint32_t step, int slot, int stage) {
+    auto store_x = [&](int slot, int stage) {
         _Float16* As = lds + stage * C::LDS_STAGE;
-        _Float16* Bs = As + C::LDS_A;
 #pragma unroll
         for (int i = 0; i < C::XPT; i++) {
             const int c = tid + NT * i;
@@ -158,136 +171,144 @@ gemm_kernel(GemmParams p) {
                     u4_t{xraw[slot][i][0], xraw[slot][i][1], xraw[slot][i][2], xraw[slot][i][3]};
             }
         }
+    };
+
+    auto decode = [&](uint32_t step, int slot, uint32_t out[NCB][16]) {
+        const uint32_t g = g_begin + step * 2 + h;
 #pragma unroll
-        for (int u = 0; u < C::UPT; u++) {
-            if (C::UNITS % NT == 0 || tid + NT * u < C::UNITS) {
-                int col, gsel, half;
-                unit_of(u, col, gsel, half);
-                const uint32_t g = g_begin + step * 2 + gsel;
-                const int lcol = (DUAL && col >= C::BN) ? col - C::BN : col;
-                const uint32_t par = Dec::parity((uint32_t)lcol * col_bytes, g);
-                if (C::HALF) {
-                    uint32_t out[8];
-                    Dec::decode_half(wraw[slot][u], par, half, out);
-                    u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + gsel * 32 + half * 16);
-                    dst[0] = u4_t{out[0], out[1], out[2], out[3]};
-                    dst[1] = u4_t{out[4], out[5], out[6], out[7]};
-                } else {
-                    uint32_t out[16];
-                    decode_group<F>(wraw[slot][u], par, out);
-                    u4_t* dst = reinterpret_cast<u4_t*>(Bs + col * kLdsRow + gsel * 32);
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        dst[j] = u4_t{out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]};
-                }
-            }
+        for (int jb = 0; jb < NCB; jb++) {
+            const uint32_t par = Dec::parity((uint32_t)bcol(jb) * col_bytes, g);
+            decode_group<F>(wraw[slot][jb], par, out[jb]);
         }
     };
 
-    f16v_t acc[TM][TN];
-    f16v_t acc2[DUAL ? TM : 1][DUAL ? TN : 1];
+    f16v_t acc[TM][NCB];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = f16v_t{};
-    if constexpr (DUAL) {
+        for (int j = 0; j < NCB; j++) acc[i][j] = f16v_t{};
+
+    const int arow = c32;
+    const int akof = 32 * h;
+    auto read_a = [&](int stage, int kk, h8_t out[TM]) {
+        const _Float16* As = lds + stage * C::LDS_STAGE;
 #pragma unroll
         for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) acc2[i][j] = f16v_t{};
-    }
-
-    const int arow = wm * TM * 32 + (lane & 31);
-    const int bcol = wn * TN * 32 + (lane & 31);
-    const int kq = (lane >> 5) * 8;
-
-    auto compute = [&](int stage) {
-        const _Float16* As = lds + stage * C::LDS_STAGE;
-        const _Float16* Bs = As + C::LDS_A;
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; kk++) {
-            h8_t a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const h8_t*>(As + (arow + i * 32) * kLdsRow + kk * 16 + kq);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                b[j] = *reinterpret_cast<const h8_t*>(Bs + (bcol + j * 32) * kLdsRow + kk * 16 + kq);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-            if constexpr (DUAL) {
-                h8_t b2[TN];
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    b2[j] = *reinterpret_cast<const h8_t*>(Bs + (C::BN + bcol + j * 32) * kLdsRow + kk * 16 + kq);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b2[j], acc2[i][j], 0, 0, 0);
-            }
-        }
+            out[i] = *reinterpret_cast<const h8_t*>(As + (arow + i * 32) * kLdsRow + akof + kk * 8);
     };
 
-    // ---- prologue: fill the P register stages, stage step 0 into LDS ----
-#pragma unroll
-    for (int j = 0; j < P; j++)
-        if ((uint32_t)j < nsteps) load_step(j, j);
-    store_step(0, 0, 0);
-    if ((uint32_t)P < nsteps) load_step(P, 0);
-    __syncthreads();
+    uint32_t bw[2][NCB][16];
+    h8_t af[2][TM];
 
-    // ---- main loop, unrolled by P so register stages are static.  Full groups
-    // of P steps run branch-free (the last group's look-ahead fetches fall out
-    // of range and read zeros), so the MFMAs of step s, the decode and LDS
-    // stores of step s+1 and the fetches of step s+1+P form one basic block
-    // that the scheduler interleaves. ----
-    uint32_t s0 = 0;
-    for (; s0 + P <= nsteps; s0 += P) {
+    // One K step, as four k-slices.  Slice kk: read the A fragments of slice
+    // kk + 1 (of step s + 1 for the last slice), the TM x NCB MFMAs of slice kk,
+    // one half-group decode of step s + 1 and a share of the memory traffic
+    // (W fetch of step s + 1 + WP, X store of step s + 2, X fetch of step s + 4).
+    // Each slice is a fenced scheduling region in which MFMAs and decode VALU
+    // ops alternate, so the decode issues while the matrix pipe is busy.
+    constexpr int NM = TM * NCB;            // MFMAs per slice
+    constexpr int HALVES = 2 * NCB;         // half-group decodes per step
+    static_assert(HALVES <= 4, "at most one half decode per slice");
+    auto step_body = [&](uint32_t s, int j) {
+        const int wslot = (j + 1) % WP;
+        uint32_t (*bn)[16] = bw[(j + 1) & 1];
+        const uint32_t gn = g_begin + (s + 1) * 2 + h;
 #pragma unroll
-        for (int j = 0; j < P; j++) {
-            const uint32_t s = s0 + j;
-            const int slot = (j + 1) % P;
-            compute(s & 1);
-            store_step(s + 1, slot, (s + 1) & 1);
-            load_step(s + 1 + P, slot);
-            __syncthreads();
-        }
-    }
+        for (int kk = 0; kk < 4; kk++) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk < 3) read_a(j % XS, kk + 1, af[(kk + 1) & 1]);
+            else read_a((j + 1) % XS, 0, af[0]);
 #pragma unroll
-    for (int j = 0; j < P; j++) {
-        const uint32_t s = s0 + j;
-        if (s < nsteps) {
-            compute(s & 1);
-            if (s + 1 < nsteps) {
-                const int slot = (j + 1) % P;
-                store_step(s + 1, slot, (s + 1) & 1);
-                if (s + 1 + P < nsteps) load_step(s + 1 + P, slot);
+            for (int jb = 0; jb < NCB; jb++) {
+                const uint32_t* bj = bw[j & 1][jb];
+                const h8_t b = __builtin_bit_cast(h8_t, u4_t{bj[4 * kk], bj[4 * kk + 1], bj[4 * kk + 2], bj[4 * kk + 3]});
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], b, acc[i][jb], 0, 0, 0);
             }
-            __syncthreads();
+            if (kk < HALVES) {
+                const int jb = kk >> 1, hh = kk & 1;
+                const uint32_t par = Dec::parity((uint32_t)bcol(jb) * col_bytes, gn);
+                decode_half_fast<F>(wraw[wslot][jb], par, hh, bn[jb] + 8 * hh);
+            }
+            if (kk == 1) store_x((j + 2) % XP, (j + 2) % XS);
+            if (kk == 2) load_x(s + 2 + XP, (j + 2) % XP);
+            __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);  // DS read
+#pragma unroll
+            for (int q = 0; q < NM; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, QR_RB_VPM, 0);  // VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (F == QUANT_Q4_K) {
+            bool slow = false;
+#pragma unroll
+            for (int jb = 0; jb < NCB; jb++)
+                slow |= needs_exact<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn));
+            if (__any(slow)) {
+#pragma unroll
+                for (int jb = 0; jb < NCB; jb++)
+                    decode_group<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn), bn[jb]);
+            }
+        }
+        load_w(s + 1 + WP, wslot);
+        __syncthreads();
+    };
+
+    // ---- prologue ----
+#pragma unroll
+    for (int t = 0; t < XP; t++) load_x(t, t);
+#pragma unroll
+    for (int t = 0; t < WP; t++) load_w(t, t);
+    store_x(0, 0);
+    store_x(1, 1);
+    load_x(XP, 0);
+    load_x(XP + 1, 1);
+    decode(0, 0, bw[0]);
+    load_w(WP, 0);
+    __syncthreads();
+    read_a(0, 0, af[0]);
+
+    // ---- main loop: full groups of U steps branch-free (look-ahead fetches past
+    // the K range read zeros), then the remainder with guards ----
+    uint32_t s0 = 0;
+    for (; s0 + U <= nsteps; s0 += U) {
+#pragma unroll
+        for (int j = 0; j < U; j++) step_body(s0 + j, j);
     }
+#pragma unroll
+    for (int j = 0; j < U; j++)
+        if (s0 + j < nsteps) step_body(s0 + j, j);
 
     // ---- split-K: publish partials, the last workgroup of the tile sums ----
+    // Workspace slot of (split z, tile): ACC / 2 float pairs per thread, pair q
+    // of thread t at q * NT + t (coalesced across lanes).  Partials cross XCDs,
+    // whose L2s are not coherent with each other: they are written and read
+    // with 64-bit agent-scope atomics (write-through / read-from-memory); the
+    // reads are issued in batches of up to 32 so their latencies overlap.
     if (ksplit > 1) {
+        constexpr int NP = C::ACC / 2;                 // float pairs per thread
+        constexpr int BATCH = NP < 32 ? NP : 32;       // pairs in flight per batch
+        static_assert(NP % BATCH == 0 && BATCH % 8 == 0, "whole 32x32 tiles per batch");
         const uint32_t T = nt_m * nt_n;
         const uint32_t tile = tmi * nt_n + tni;
-        float* slot = p.ws + ((size_t)kz * T + tile) * (C::ACC * NT) + tid;
-        int e = 0;
+        auto pair_ptr = [&](uint32_t z) {
+            return reinterpret_cast<uint64_t*>(p.ws) + ((size_t)z * T + tile) * (NP * NT) + tid;
+        };
+        {
+            uint64_t* dst = pair_ptr(kz);
+            int q = 0;
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++)
+                for (int j = 0; j < NCB; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++, e++) {
-                    __hip_atomic_store(slot + e * NT, acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if constexpr (DUAL)
-                        __hip_atomic_store(slot + (C::ACC / 2 + e) * NT, acc2[i][j][r], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
+                    for (int r = 0; r < 16; r += 2, q++) {
+                        const uint64_t v = (uint64_t)f32_bits(acc[i][j][r]) | ((uint64_t)f32_bits(acc[i][j][r + 1]) << 32);
+                        __hip_atomic_store(dst + q * NT, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+        }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
         __syncthreads();
         __shared__ uint32_t s_last;
@@ -302,65 +323,64 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                acc[i][j] = f16v_t{};
-                if constexpr (DUAL) acc2[i][j] = f16v_t{};
-            }
+            for (int j = 0; j < NCB; j++) acc[i][j] = f16v_t{};
         for (uint32_t z = 0; z < ksplit; z++) {
-            const float* src = p.ws + ((size_t)z * T + tile) * (C::ACC * NT) + tid;
-            int e2 = 0;
+            const uint64_t* src = pair_ptr(z);
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+            for (int q0 = 0; q0 < NP; q0 += BATCH) {
+                uint64_t t[BATCH];
 #pragma unroll
-                for (int j = 0; j < TN; j++)
+                for (int q = 0; q < BATCH; q++)
+                    t[q] = __hip_atomic_load(src + (q0 + q) * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-                    for (int r = 0; r < 16; r++, e2++) {
-                        acc[i][j][r] += __hip_atomic_load(src + e2 * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        if constexpr (DUAL)
-                            acc2[i][j][r] += __hip_atomic_load(src + (C::ACC / 2 + e2) * NT, __ATOMIC_RELAXED,
-                                                               __HIP_MEMORY_SCOPE_AGENT);
-                    }
+                for (int q = 0; q < BATCH; q++) {
+                    const int qq = q0 + q;               // pair index: tile qq / 8, rows 2 (qq % 8)
+                    const int i = (qq / 8) / NCB, j = (qq / 8) % NCB, r = 2 * (qq % 8);
+                    acc[i][j][r] += bits_f32((uint32_t)t[q]);
+                    acc[i][j][r + 1] += bits_f32((uint32_t)(t[q] >> 32));
+                }
+            }
         }
         if (tid == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // ---- epilogue: accumulator element r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
-    // column l%32 of the 32x32 MFMA tile.  The (SwiGLU-combined) fp32 values go
-    // through LDS, one 32-row band of the wave tile at a time, so that each
-    // lane then owns 8 consecutive columns of one row: the residual is read and
-    // the output written with 16-byte accesses, and the value is rounded to
-    // fp16 once, after the residual add. ----
+    // ---- epilogue: accumulator element r of lane l is row 8 (r / 4) + 4 (l / 32)
+    // + r % 4, column l % 32 of its 32x32 tile.  Values (SwiGLU-combined) go
+    // through LDS one 32-row band of the wave tile at a time, so each lane then
+    // owns 8 consecutive columns of one row: residual read and output written
+    // with 16-byte accesses, one rounding to fp16 after the residual add. ----
     auto value = [&](int i, int j, int r) {
         float v = acc[i][j][r];
         if constexpr (DUAL) {
-            const float u = acc2[i][j][r];
+            const float u = acc[i][j + TN][r];
             v = v / (1.0f + __expf(-v)) * u;
         }
         return v;
     };
+    const int wcol0 = n0 + wave * C::WN;
     const bool vec_io = ((reinterpret_cast<uintptr_t>(p.Y) | reinterpret_cast<uintptr_t>(p.R)) & 15u) == 0 &&
                         (N & 7u) == 0 && (p.head_D & 7u) == 0;
     if (vec_io) {
-        constexpr int WC = TN * 32;        // wave tile columns
-        constexpr int ERS = WC + 4;        // padded LDS row (floats)
-        static_assert(WGM * WGN * 32 * ERS * 4 <= 2 * C::LDS_STAGE * 2, "epilogue staging fits the LDS stages");
+        constexpr int WC = C::WN;
+        constexpr int ERS = WC + 4;  // padded LDS row (floats)
+        static_assert(NW * 32 * ERS * 4 <= C::LDS_BYTES, "epilogue staging fits the LDS allocation");
         float* E = reinterpret_cast<float*>(lds) + wave * 32 * ERS;
-        __syncthreads();  // every wave is done with the operand stages
+        __syncthreads();  // every wave is done with the X stages
 #pragma unroll
         for (int i = 0; i < TM; i++) {
 #pragma unroll
             for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++)
-                    E[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ERS + j * 32 + (lane & 31)] = value(i, j, r);
+                    E[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ERS + j * 32 + c32] = value(i, j, r);
             __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes done (wave-local region)
             __builtin_amdgcn_wave_barrier();
-            constexpr int CHUNKS = 32 * WC / 8;  // 8-column chunks in the band
+            constexpr int CHUNKS = 32 * WC / 8;
 #pragma unroll
             for (int c = lane; c < CHUNKS; c += 64) {
                 const int row = c / (WC / 8), c8 = c % (WC / 8);
-                const int m = m0 + wm * TM * 32 + i * 32 + row;
-                const int n = n0 + wn * WC + c8 * 8;
+                const int m = m0 + i * 32 + row;
+                const int n = wcol0 + c8 * 8;
                 if (m < (int)M && n < (int)N) {
                     const f4_t lo = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8);
                     const f4_t hi = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8 + 4);
@@ -370,9 +390,9 @@ gemm_kernel(GemmParams p) {
                         const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
-                            const h2_t h = as_h2(rw[q]);
-                            v[2 * q] += (float)h.x;
-                            v[2 * q + 1] += (float)h.y;
+                            const h2_t hh = as_h2(rw[q]);
+                            v[2 * q] += (float)hh.x;
+                            v[2 * q + 1] += (float)hh.y;
                         }
                     }
                     u4_t o;
@@ -382,8 +402,8 @@ gemm_kernel(GemmParams p) {
                     o.w = pack_h2(f2h_bits(v[6]), f2h_bits(v[7]));
                     size_t off;
                     if (p.head_D) {
-                        const uint32_t h = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
-                        off = ((size_t)h * M + m) * p.head_D + dd;
+                        const uint32_t hd = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
+                        off = ((size_t)hd * M + m) * p.head_D + dd;
                     } else {
                         off = (size_t)m * N + n;
                     }
@@ -398,17 +418,17 @@ gemm_kernel(GemmParams p) {
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn * TN * 32 + j * 32 + (lane & 31);
+            const int n = wcol0 + j * 32 + c32;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * TM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < (int)M && n < (int)N) {
                     float v = value(i, j, r);
                     if (p.R) v += (float)p.R[(size_t)m * N + n];
                     size_t o;
                     if (p.head_D) {
-                        const uint32_t h = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
-                        o = ((size_t)h * M + m) * p.head_D + dd;
+                        const uint32_t hd = (uint32_t)n / p.head_D, dd = (uint32_t)n % p.head_D;
+                        o = ((size_t)hd * M + m) * p.head_D + dd;
                     } else {
                         o = (size_t)m * N + n;
                     }
@@ -418,122 +438,104 @@ gemm_kernel(GemmParams p) {
         }
 }
 
-#ifndef QR_GEMM_STAGES
-#define QR_GEMM_STAGES 3
+
+// Shapes {TM, TN, NW}: BM = 32 TM, BN = 32 TN NW.
+//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K: QR_RB_BIG_K,
+//                  default 4, 1, 8 -> 128 x 256 with two waves per SIMD, whose
+//                  heavier decode then overlaps the other wave's MFMAs)
+//   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
+//                  of 128 x 256 at the same K split, half the reduction)
+//   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
+#ifndef QR_RB_BIG
+#define QR_RB_BIG 4, 2, 4
 #endif
-
-// Tile configurations: {waves_m, waves_n, tiles_m, tiles_n} -> BM x BN.
-//   0: 8 waves 4x2, 2x2 tiles -> 256 x 128  (large M)
-//   1: 4 waves 2x2, 2x2 tiles -> 128 x 128  (medium M)
-//   2: 4 waves 2x2, 1x2 tiles ->  64 x 128
-//   dual (SwiGLU): 3: 8 waves 4x2, 2x1 -> 256 x 64 (gate + up: 128 weight
-//   columns per step); 4: 4 waves 2x2, 1x1 -> 64 x 64
-static int pick_shape(uint32_t M, bool dual) {
-    if (dual) return M > 64 ? 3 : 4;
-    if (M >= 1024) return 0;
-    if (M > 64) return 1;
-    return 2;
+#ifndef QR_RB_BIG_K
+#define QR_RB_BIG_K 4, 1, 8
+#endif
+#ifndef QR_RB_MID
+#define QR_RB_MID 4, 1, 4
+#endif
+template <int TM, int TN, int NW> struct ShapeOf {
+    static constexpr uint32_t bm = 32 * TM, bn = 32 * TN * NW;
+};
+struct RbShape {
+    uint32_t bm, bn;
+};
+static int rb_pick(int format, uint32_t M, bool dual) {
+    if (dual) return 2;
+    if (M >= 1024) return format == QUANT_Q4_K ? 3 : 0;
+    return 1;
 }
-
-static void shape_dims(int shape, uint32_t& bm, uint32_t& bn) {
-    switch (shape) {
-        case 0: bm = 256; bn = 128; return;
-        case 1: bm = 128; bn = 128; return;
-        case 2: bm = 64; bn = 128; return;
-        case 3: bm = 256; bn = 64; return;
-        default: bm = 64; bn = 64; return;
+static RbShape rb_dims(int s) {
+    switch (s) {
+        case 0: return {ShapeOf<QR_RB_BIG>::bm, ShapeOf<QR_RB_BIG>::bn};
+        case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
+        case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
+        default: return {128, 128};
     }
 }
 
-template <int F, int WGM, int WGN, int TM, int TN, bool DUAL>
-static hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
-    using C = GemmCfg<F, WGM, WGN, TM, TN, DUAL>;
-    auto kern = gemm_kernel<F, WGM, WGN, TM, TN, DUAL, QR_GEMM_STAGES>;
-    const size_t lds = 2 * C::LDS_STAGE * sizeof(_Float16);
-    static bool attr_set = false;  // per instantiation
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+template <int F, int TM, int TN, int NW, bool DUAL>
+static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
+    using C = rb::Cfg<TM, TN, NW, DUAL>;
+    auto kern = gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES>;
+    const size_t lds = C::LDS_BYTES;
     const uint32_t T = ((p.M + C::BM - 1) / C::BM) * ((p.N + C::BN - 1) / C::BN);
     const uint32_t ks = p.ksplit ? p.ksplit : 1;
     hipLaunchKernelGGL(kern, dim3(T, ks), dim3(C::NT), lds, st, p);
     return hipGetLastError();
 }
 
-// Kernel selection: the register-B kernel (qr_gemm_rb.hip) unless
-// QR_GEMM_IMPL=lds selects the LDS-staged one.
-static bool use_rb() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("QR_GEMM_IMPL");
-        v = (e && e[0] == 'l') ? 0 : 1;
-    }
-    return v == 1;
-}
-
-uint32_t gemm_pick_ksplit(const GemmParams& p) {
-    if (use_rb()) return gemm_rb_pick_ksplit(p);
-    const bool dual = p.W2 != nullptr;
-    if (dual) return 1;
-    uint32_t bm, bn;
-    shape_dims(pick_shape(p.M, dual), bm, bn);
-    const uint32_t T = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-    uint32_t ks = 1;
-    // split K until the grid covers the 256 CUs; each split keeps >= 1024 of K
-    // and a whole number of 256-element super-blocks
-    while (T * ks < 256 && p.K % (256 * ks * 2) == 0 && p.K / (ks * 2) >= 1024) ks *= 2;
-    return ks;
-}
-
-size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
-    if (use_rb()) return gemm_rb_workspace_floats(p, ks, tiles);
-    uint32_t bm, bn;
-    const bool dual = p.W2 != nullptr;
-    shape_dims(pick_shape(p.M, dual), bm, bn);
-    const uint32_t T = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-    if (tiles) *tiles = T;
-    return ks > 1 ? (size_t)ks * T * bm * bn * (dual ? 2 : 1) : 0;
-}
-
 template <int F, bool DUAL>
-static hipError_t launch_fmt(const GemmParams& p, hipStream_t st) {
+static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
     if constexpr (DUAL) {
-#ifndef QR_DUAL_CFG
-#define QR_DUAL_CFG 2
-#endif
-        if (pick_shape(p.M, true) == 3) {
-            if (QR_DUAL_CFG == 1) return launch_cfg<F, 2, 2, 2, 1, true>(p, st);
-            if (QR_DUAL_CFG == 2) return launch_cfg<F, 4, 2, 2, 1, true>(p, st);
-            if (QR_DUAL_CFG == 3) return launch_cfg<F, 2, 2, 2, 2, true>(p, st);
-            return launch_cfg<F, 4, 2, 1, 1, true>(p, st);
-        }
-        return launch_cfg<F, 2, 2, 1, 1, true>(p, st);
+        return rb_launch_cfg<F, 4, 1, 4, true>(p, st);
     } else {
-        switch (pick_shape(p.M, false)) {
-            case 0: return launch_cfg<F, 4, 2, 2, 2, false>(p, st);
-            case 1: return launch_cfg<F, 2, 2, 2, 2, false>(p, st);
-            default: return launch_cfg<F, 2, 2, 1, 2, false>(p, st);
+        switch (rb_pick(F, p.M, false)) {
+            case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);
+            case 3: return rb_launch_cfg<F, QR_RB_BIG_K, false>(p, st);
+            default: return rb_launch_cfg<F, QR_RB_MID, false>(p, st);
         }
     }
 }
 
 hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
-    if (use_rb()) {
-        GemmParams p = p0;
-        p.group_m = gemm_rb_group_m(p);
-        return launch_gemm_rb(p, st);
-    }
-    const GemmParams& p = p0;
+    GemmParams p = p0;
+    p.group_m = gemm_group_m(p);
     const bool dual = p.W2 != nullptr;
     switch (p.format) {
-        case QUANT_Q4_0: return dual ? launch_fmt<QUANT_Q4_0, true>(p, st) : launch_fmt<QUANT_Q4_0, false>(p, st);
-        case QUANT_MLX_4BIT: return dual ? launch_fmt<QUANT_MLX_4BIT, true>(p, st) : launch_fmt<QUANT_MLX_4BIT, false>(p, st);
-        case QUANT_Q4_K: return dual ? launch_fmt<QUANT_Q4_K, true>(p, st) : launch_fmt<QUANT_Q4_K, false>(p, st);
-        case QUANT_TERNARY_1_58: return dual ? launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
+        case QUANT_Q4_0: return dual ? rb_launch_fmt<QUANT_Q4_0, true>(p, st) : rb_launch_fmt<QUANT_Q4_0, false>(p, st);
+        case QUANT_MLX_4BIT: return dual ? rb_launch_fmt<QUANT_MLX_4BIT, true>(p, st) : rb_launch_fmt<QUANT_MLX_4BIT, false>(p, st);
+        case QUANT_Q4_K: return dual ? rb_launch_fmt<QUANT_Q4_K, true>(p, st) : rb_launch_fmt<QUANT_Q4_K, false>(p, st);
+        case QUANT_TERNARY_1_58: return dual ? rb_launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : rb_launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
         default: return hipErrorInvalidValue;
     }
 }
 
+uint32_t gemm_pick_ksplit(const GemmParams& p) {
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
+    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+    // One workgroup fits a CU (its registers), so the grid runs in waves of
+    // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
+    // >= 512 of K per split) while the grid still fits one such wave.
+    uint32_t ks = 1;
+    while (T * ks * 2 <= 256 && p.K % (256 * ks * 2) == 0 && p.K / (ks * 2) >= 512) ks *= 2;
+    return ks;
+}
+
+size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
+    const bool dual = p.W2 != nullptr;
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, dual));
+    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+    if (tiles) *tiles = T;
+    return ks > 1 ? (size_t)ks * T * d.bm * d.bn * (dual ? 2 : 1) : 0;
+}
+
+uint32_t gemm_group_m(const GemmParams& p) {
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
+    const uint32_t nt_m = (p.M + d.bm - 1) / d.bm;
+    return nt_m >= 4 ? 4u : 2u;
+}
+
 }  // namespace qr
+

@@ -26,10 +26,7 @@ struct GemmParams {
 };
 
 hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
-hipError_t launch_gemm_rb(const GemmParams& p, hipStream_t st);
-uint32_t gemm_rb_pick_ksplit(const GemmParams& p);
-size_t gemm_rb_workspace_floats(const GemmParams& p, uint32_t ksplit, uint32_t* tiles);
-uint32_t gemm_rb_group_m(const GemmParams& p);
+uint32_t gemm_group_m(const GemmParams& p);
 uint32_t gemm_pick_ksplit(const GemmParams& p);
 size_t gemm_workspace_floats(const GemmParams& p, uint32_t ksplit, uint32_t* tiles);
 
