@@ -118,7 +118,7 @@ def bench_projection(b, timer, name, fmt, M, K, N, seed):
 
     Xn = synth.activations(M, K, seed)
     X = torch.from_numpy(Xn).cuda()
-    Wn = synth.quantized_weights(fmt, N, K, seed + 1)
+    Wn = synth.quantized_weights(fmt, N, K, seed + 1) if fmt < 4 else synth.random_blocks(fmt, N, K, seed + 1)
     W0 = torch.from_numpy(Wn).cuda()
     Ws = rotated(W0, W0.numel())
     Y = torch.empty(M, N, dtype=torch.float16, device="cuda")
@@ -319,7 +319,7 @@ def main():
         per["cfg3_q4_k_m2048"], _ = bench_projection(b, timer, "cfg3_q4_k_m2048", 2, 2048, 4096, 4096, 30)
     if on("cfg4_ternary_m129"):
         per["cfg4_ternary_m129"], _ = bench_projection(b, timer, "cfg4_ternary_m129", 3, 129, 2048, 8192, 40)
-    for fmt, tag in ((0, "q4_0"), (1, "mlx"), (3, "ternary")):
+    for fmt, tag in ((0, "q4_0"), (1, "mlx"), (3, "ternary"), (4, "var_rate"), (5, "exl3")):
         name = f"m2048_k4096_{tag}"
         if want is not None and name in want:
             per[name], _ = bench_projection(b, timer, name, fmt, 2048, 4096, 4096, 60 + fmt)

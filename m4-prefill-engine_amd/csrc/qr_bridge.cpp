@@ -118,7 +118,7 @@ void sync_and_release() {
 }
 
 bool is_projection_format(int f) { return f >= 0 && f < 6; }
-bool has_kernels(int f) { return f >= 0 && f < 4; }
+bool has_kernels(int f) { return f >= 0 && f < 6; }
 
 // core/bridge/m4_mlx_bridge.mm:204-230, minus the init check.
 int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, size_t Yb, int format,

@@ -230,6 +230,143 @@ template <> struct Decoder<QUANT_TERNARY_1_58> {
     __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
 };
 
+// --------------------------------------------------------------------------
+// Formats whose CPU gold forms each weight with double-precision roundings
+// (VAR_RATE_AFFINE, EXL3): the weight is computed here with the same double
+// operations -- every product involved is exact in double, so fused and
+// separate multiply-add round identically -- and then rounded ONCE to
+// binary16: the double is narrowed to float with round-to-odd (>= 2 spare
+// bits), whose RNE conversion to binary16 equals RNE of the double.
+// --------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t rne16_from_f64(double w) {
+    const float f = (float)w;
+    uint32_t bits = f32_bits(f);
+    const double back = (double)f;
+    if (back != w) {
+        const bool away = __builtin_fabs(back) > __builtin_fabs(w);
+        bits = (away ? bits - 1u : bits) | 1u;
+    }
+    return f2h_bits(bits_f32(bits));
+}
+
+// Code j (0..31) of an LSB-first bit stream of B-bit codes held in `q`.
+// (j is a compile-time constant after unrolling: the second word is read only
+// when the code straddles a word boundary.)
+template <int B>
+__device__ __forceinline__ uint32_t stream_code(const uint32_t* q, int j) {
+    const int bit = j * B, w = bit >> 5, sh = bit & 31;
+    uint32_t v = q[w] >> sh;
+    if (sh + B > 32) v |= q[w + 1] << (32 - sh);
+    return v & ((1u << B) - 1u);
+}
+
+// --------------------------------------------------------------------------
+// VAR_RATE_AFFINE: 160-byte super-blocks of 8 sub-blocks of 32
+// (cpu_gold_reference.h:212-323).  Sub-block s: scale S = d sc / 16, bias
+// B = bias + d (bi - 128) / 16; mode bits 0..2 = code depth (3 and 5: LSB-first
+// bit streams of 12 / 20 bytes; anything else: 4-bit, byte i low nibble ->
+// code i, high -> code i + 16), bits 3..4 = order (1: code j multiplies
+// element ((j & 1) << 4) | (j >> 1); 2: element 31 - j; else element j).
+// w = (q - 2^(depth-1)) S + B.  Raw words: header dwords 0..6 (d | bias,
+// scales, biases, modes), then 5 code dwords from byte 32 + offset[s].
+// --------------------------------------------------------------------------
+template <> struct Decoder<QUANT_VAR_RATE_AFFINE> {
+    static constexpr int kBlockElems = 32;
+    static constexpr int kBlockBytes = 160;
+    static constexpr int kRawWords = 12;
+    // sub-block payload offsets {0, 12, 24, 40, 56, 72, 88, 108}, one per byte
+    static constexpr uint64_t kOffsets = 0x6C58483828180C00ull;
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[12]) {
+        const uint32_t o = col_off + (kb >> 3) * 160u;
+        const u4_t h0 = ld_b128(r, o);
+        const u4_t h1 = ld_b128(r, o + 16u);
+        raw[0] = h0.x; raw[1] = h0.y; raw[2] = h0.z; raw[3] = h0.w;
+        raw[4] = h1.x; raw[5] = h1.y; raw[6] = h1.z;
+        const uint32_t q = o + 32u + (uint32_t)((kOffsets >> (8u * (kb & 7u))) & 0xffu);  // 4-byte aligned
+#pragma unroll
+        for (int i = 0; i < 5; i++) raw[7 + i] = ld_b32(r, q + 4u * i);
+    }
+    __device__ static uint32_t byte_of(const uint32_t* w, uint32_t i) { return (w[i >> 2] >> (8u * (i & 3u))) & 0xffu; }
+    // code j of the sub-block at depth 3, 5 or 4 (j compile-time after unrolling)
+    __device__ __forceinline__ static uint32_t code(const uint32_t* q, bool d3, bool d5, int j) {
+        const uint32_t c4 = j < 16 ? (byte_of(q, (uint32_t)j) & 15u) : (byte_of(q, (uint32_t)(j - 16)) >> 4);
+        return d3 ? stream_code<3>(q, j) : (d5 ? stream_code<5>(q, j) : c4);
+    }
+    __device__ __forceinline__ static void decode_half(const uint32_t raw[12], uint32_t s, int h, uint32_t out[8]) {
+        const double d = (double)h2f(raw[0] & 0xffffu), bias = (double)h2f(raw[0] >> 16);
+        const uint32_t sc = (uint32_t)((((uint64_t)raw[2] << 32) | raw[1]) >> (8u * s)) & 0xffu;
+        const uint32_t bi = (uint32_t)((((uint64_t)raw[4] << 32) | raw[3]) >> (8u * s)) & 0xffu;
+        const uint32_t mode = (uint32_t)((((uint64_t)raw[6] << 32) | raw[5]) >> (8u * s)) & 0xffu;
+        const double S = d * (double)sc * 0.0625;
+        const double B = bias + d * ((double)bi - 128.0) * 0.0625;
+        const uint32_t depth = mode & 7u, order = (mode >> 3) & 3u;
+        const uint32_t* q = raw + 7;
+        const bool d3 = depth == 3u, d5 = depth == 5u;
+        const double zero = d3 ? 4.0 : (d5 ? 16.0 : 8.0);
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            uint32_t hw[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int p = 16 * h + e + t;                      // element (activation) index
+                const int j1 = p < 16 ? 2 * p : 2 * (p - 16) + 1;  // order 1: code that lands on p
+                const uint32_t c = order == 1u ? code(q, d3, d5, j1) : (order == 2u ? code(q, d3, d5, 31 - p) : code(q, d3, d5, p));
+                hw[t] = rne16_from_f64(__builtin_fma((double)c - zero, S, B));
+            }
+            out[e >> 1] = hw[0] | (hw[1] << 16);
+        }
+    }
+    __device__ static uint32_t parity(uint32_t, uint32_t kb) { return kb & 7u; }
+};
+
+// --------------------------------------------------------------------------
+// EXL3: 144-byte super-blocks of 8 sub-blocks of 32 (cpu_gold_reference.h:
+// 345-392).  Sub-block s: S = d sc / 64, R = d (res - 128) / 128; 3-bit codes
+// q (LSB-first stream, 12 bytes at byte 48 + 12 s); int8 codebook cb[16];
+// w = (bias + S cb[q]) + R cb[q + 8].  Raw words: header dwords 0..8 (d | bias,
+// scales, residuals, codebook), then the 3 code dwords.
+// --------------------------------------------------------------------------
+template <> struct Decoder<QUANT_EXL3> {
+    static constexpr int kBlockElems = 32;
+    static constexpr int kBlockBytes = 144;
+    static constexpr int kRawWords = 12;
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[12]) {
+        const uint32_t o = col_off + (kb >> 3) * 144u;
+        const u4_t h0 = ld_b128(r, o);
+        const u4_t h1 = ld_b128(r, o + 16u);
+        raw[0] = h0.x; raw[1] = h0.y; raw[2] = h0.z; raw[3] = h0.w;
+        raw[4] = h1.x; raw[5] = h1.y; raw[6] = h1.z; raw[7] = h1.w;
+        raw[8] = ld_b32(r, o + 32u);
+        const uint32_t q = o + 48u + 12u * (kb & 7u);
+        raw[9] = ld_b32(r, q);
+        raw[10] = ld_b32(r, q + 4u);
+        raw[11] = ld_b32(r, q + 8u);
+    }
+    __device__ __forceinline__ static void decode_half(const uint32_t raw[12], uint32_t s, int h, uint32_t out[8]) {
+        const double d = (double)h2f(raw[0] & 0xffffu), bias = (double)h2f(raw[0] >> 16);
+        const uint32_t sc = (uint32_t)((((uint64_t)raw[2] << 32) | raw[1]) >> (8u * s)) & 0xffu;
+        const uint32_t rs = (uint32_t)((((uint64_t)raw[4] << 32) | raw[3]) >> (8u * s)) & 0xffu;
+        const double S = d * (double)sc * 0.015625;
+        const double R = d * ((double)rs - 128.0) * 0.0078125;
+        // codebook bytes 20..35 = raw[5] .. raw[8]: base cb[0..7] in raw[5], raw[6],
+        // residual cb[8..15] in raw[7], raw[8]
+        const uint32_t* q = raw + 9;
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            uint32_t hw[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t code = stream_code<3>(q, 16 * h + e + t);
+                const int cb0 = (int)(int8_t)(perm(raw[6], raw[5], code) & 0xffu);
+                const int cb1 = (int)(int8_t)(perm(raw[8], raw[7], code) & 0xffu);
+                hw[t] = rne16_from_f64(__builtin_fma(R, (double)cb1, __builtin_fma(S, (double)cb0, bias)));
+            }
+            out[e >> 1] = hw[0] | (hw[1] << 16);
+        }
+    }
+    __device__ static uint32_t parity(uint32_t, uint32_t kb) { return kb & 7u; }
+};
+
 // Branch-free half-group decode for pipelined callers: bit-exact whenever no
 // lane of the wave has needs_exact() true for its group (Q4_K and Q4_0 have a
 // slow path; callers check and re-decode with decode_group otherwise).

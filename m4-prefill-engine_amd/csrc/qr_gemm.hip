@@ -508,6 +508,8 @@ hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
         case QUANT_MLX_4BIT: return dual ? rb_launch_fmt<QUANT_MLX_4BIT, true>(p, st) : rb_launch_fmt<QUANT_MLX_4BIT, false>(p, st);
         case QUANT_Q4_K: return dual ? rb_launch_fmt<QUANT_Q4_K, true>(p, st) : rb_launch_fmt<QUANT_Q4_K, false>(p, st);
         case QUANT_TERNARY_1_58: return dual ? rb_launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : rb_launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
+        case QUANT_VAR_RATE_AFFINE: return dual ? rb_launch_fmt<QUANT_VAR_RATE_AFFINE, true>(p, st) : rb_launch_fmt<QUANT_VAR_RATE_AFFINE, false>(p, st);
+        case QUANT_EXL3: return dual ? rb_launch_fmt<QUANT_EXL3, true>(p, st) : rb_launch_fmt<QUANT_EXL3, false>(p, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import numpy as np
 
-Q4_0, MLX_4BIT, Q4_K, TERNARY_1_58 = 0, 1, 2, 3
+Q4_0, MLX_4BIT, Q4_K, TERNARY_1_58, VAR_RATE_AFFINE, EXL3 = 0, 1, 2, 3, 4, 5
 BLOCK_ELEMS = {0: 32, 1: 32, 2: 256, 3: 32, 4: 256, 5: 256, 6: 32, 7: 128}
 BLOCK_BYTES = {0: 18, 1: 20, 2: 144, 3: 12, 4: 160, 5: 144, 6: 34, 7: 34}
 
@@ -218,8 +218,77 @@ def random_blocks(fmt: int, N: int, K: int, seed: int, code3: bool = False) -> n
         codes = rng.integers(0, 4 if code3 else 3, (N, nb, 32), dtype=np.uint8)
         d = (rng.random((N, nb)) * 0.05 + 0.01).astype(np.float32)
         return _pack_ternary(codes, d)
+    elif fmt == VAR_RATE_AFFINE:
+        return var_rate_blocks(N, K, seed)
+    elif fmt == EXL3:
+        return exl3_blocks(N, K, seed)
     else:
         raise ValueError(f"no random generator for format {fmt}")
+    return out.reshape(-1)
+
+
+VAR_OFFSETS = (0, 12, 24, 40, 56, 72, 88, 108)   # quant_router_kernels.metal:285 / bench:107
+VAR_BITS = (3, 3, 4, 4, 4, 4, 5, 5)              # bench_universal_router.mm:108
+
+
+def _pack_stream(q: np.ndarray, bits: int) -> np.ndarray:
+    """q [..., 8] codes of `bits` bits -> [..., bits] bytes holding them as one
+    LSB-first bit stream (the byte packing of bench_universal_router.mm:124-152,
+    written as a stream)."""
+    v = np.zeros(q.shape[:-1], np.uint64)
+    for i in range(8):
+        v |= q[..., i].astype(np.uint64) << np.uint64(bits * i)
+    return np.stack([((v >> np.uint64(8 * b)) & np.uint64(0xff)).astype(np.uint8) for b in range(bits)], -1)
+
+
+def var_rate_blocks(N: int, K: int, seed: int, codes_out: dict | None = None, modes=None) -> np.ndarray:
+    """VAR_RATE_AFFINE super-blocks as bench_universal_router.mm:105-158 draws
+    them: d in [0.0004, 0.0044), bias in [-0.005, 0.005), sub-block scales
+    10..209, biases 0..254, depths {3,3,4,4,4,4,5,5} and orders s % 3, random
+    codes.  `modes` [8] overrides the mode bytes (depth | order << 3) -- the
+    payload is still laid out by the standard depths.  If `codes_out` is a
+    dict, the drawn codes [N, nb, 8, 32] (stream order j) are stored in it."""
+    rng = np.random.default_rng(seed)
+    nb = K // 256
+    out = np.zeros((N, nb, 160), np.uint8)
+    out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.004 + 0.0004).astype(np.float32))
+    out[..., 2:4] = _h16_bytes((rng.random((N, nb)) * 0.01 - 0.005).astype(np.float32))
+    out[..., 4:12] = (rng.random((N, nb, 8)) * 200.0 + 10.0).astype(np.uint8)
+    out[..., 12:20] = (rng.random((N, nb, 8)) * 255.0).astype(np.uint8)
+    out[..., 20:28] = np.array(modes if modes is not None else [((s % 3) << 3) | VAR_BITS[s] for s in range(8)],
+                               np.uint8)
+    codes = np.zeros((N, nb, 8, 32), np.uint8)
+    for s in range(8):
+        bits, off = VAR_BITS[s], 32 + VAR_OFFSETS[s]
+        q = rng.integers(0, 1 << bits, (N, nb, 32), dtype=np.uint8)
+        codes[:, :, s] = q
+        if bits == 4:
+            out[..., off:off + 16] = _pack_nibbles32(q)
+        else:
+            out[..., off:off + 4 * bits] = _pack_stream(q.reshape(N, nb, 4, 8), bits).reshape(N, nb, 4 * bits)
+    if codes_out is not None:
+        codes_out["codes"] = codes
+    return out.reshape(-1)
+
+
+def exl3_blocks(N: int, K: int, seed: int, codes_out: dict | None = None) -> np.ndarray:
+    """EXL3 super-blocks as bench_universal_router.mm:160-193 draws them:
+    d in [0.0002, 0.0022), bias in [-0.0025, 0.0025), codebook (c - 3.5) * 8
+    and (c - 3.5) * 3 (truncated to int8), scales 10..129, residuals 0..254,
+    random 3-bit codes."""
+    rng = np.random.default_rng(seed)
+    nb = K // 256
+    out = np.zeros((N, nb, 144), np.uint8)
+    out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.002 + 0.0002).astype(np.float32))
+    out[..., 2:4] = _h16_bytes((rng.random((N, nb)) * 0.005 - 0.0025).astype(np.float32))
+    out[..., 4:12] = (rng.random((N, nb, 8)) * 120.0 + 10.0).astype(np.uint8)
+    out[..., 12:20] = (rng.random((N, nb, 8)) * 255.0).astype(np.uint8)
+    cb = np.array([np.trunc((c - 3.5) * 8.0) for c in range(8)] + [np.trunc((c - 3.5) * 3.0) for c in range(8)])
+    out[..., 20:36] = cb.astype(np.int8).view(np.uint8)
+    q = rng.integers(0, 8, (N, nb, 8, 32), dtype=np.uint8)
+    out[..., 48:144] = _pack_stream(q.reshape(N, nb, 8, 4, 8), 3).reshape(N, nb, 96)
+    if codes_out is not None:
+        codes_out["codes"] = q
     return out.reshape(-1)
 
 

@@ -53,12 +53,15 @@ def weights(kind, fmt, N, K, seed):
 # Dequantization: bit-exact
 # --------------------------------------------------------------------------
 
-@pytest.mark.parametrize("fmt,K", [(0, 512), (0, 96), (1, 512), (1, 96), (2, 512), (3, 512), (3, 96)])
+@pytest.mark.parametrize("fmt,K", [(0, 512), (0, 96), (1, 512), (1, 96), (2, 512), (3, 512), (3, 96), (4, 512),
+                                   (5, 512)])
 @pytest.mark.parametrize("kind", ["random", "quantized"])
 def test_dequant_bit_exact(bridge, oracle, fmt, K, kind):
     N = 72
     if kind == "quantized" and fmt == 1 and K % 64:
         pytest.skip("MLX g64 quantizer needs K % 64 == 0")
+    if kind == "quantized" and fmt >= 4:
+        pytest.skip("VAR_RATE_AFFINE / EXL3 come from the reference's random generators only")
     W = weights(kind, fmt, N, K, 100 + fmt)
     out = empty16(N, K)
     bridge.dequantize(dev(W), out, fmt, K, N)
@@ -81,6 +84,53 @@ def test_dequant_ternary_code3_and_q4k_slow_path(bridge, oracle):
     bridge.synchronize()
     np.testing.assert_array_equal(host(out).view(np.uint16), oracle.dequantize(3, W, 256, 40).view(np.uint16))
     np.testing.assert_array_equal(host(outk).view(np.uint16), oracle.dequantize(2, Wk, 512, 40).view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [4, 5])
+def test_dequant_double_rounding_formats_wide_scales(bridge, oracle, fmt):
+    """VAR_RATE_AFFINE / EXL3 weights are formed in double by the CPU gold and
+    rounded once to fp16: scales and biases spread over the whole binary16
+    range exercise the round-to-odd narrowing (inexact double -> float) and
+    subnormal / overflowing results; mixed depths and orders per lane."""
+    N, K = 96, 512
+    rng = np.random.default_rng(40 + fmt)
+    W = synth.random_blocks(fmt, N, K, 41 + fmt).reshape(N, K // 256, -1).copy()
+    mag = 2.0 ** rng.integers(-24, 12, (N, K // 256, 2))
+    sign = np.where(rng.random((N, K // 256, 2)) < 0.5, -1.0, 1.0)
+    hdr = (sign * mag * (1 + rng.random((N, K // 256, 2)))).astype(np.float16)
+    W[..., 0:4] = hdr.view(np.uint8).reshape(N, K // 256, 4)
+    if fmt == 4:  # random depths (including values that mean 4-bit) and orders per sub-block
+        W[..., 20:28] = rng.integers(0, 32, (N, K // 256, 8)).astype(np.uint8)
+    W = W.reshape(-1)
+    out = empty16(N, K)
+    bridge.dequantize(dev(W), out, fmt, K, N)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(out).view(np.uint16), oracle.dequantize(fmt, W, K, N).view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [4, 5])
+@pytest.mark.parametrize("M,K,N", [(1, 512, 256), (33, 512, 256), (129, 512, 256), (128, 4096, 320)])
+def test_gemm_var_rate_and_exl3(bridge, oracle, fmt, M, K, N):
+    """tests/e2e/test_tier1_feature_coverage.mm:382-460 shapes plus a split-K
+    shape; standard, residual and direct-head outputs."""
+    X = synth.activations(M, K, 80 + M, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 81 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    R = synth.activations(M, N, 82)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    H, D = N // 64, 64
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    bridge.synchronize()
+    axw = absxw(oracle, fmt, X, W, K, N)
+    ref = oracle.gemm(fmt, X, W, N)
+    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, axw, K))
+    refr = oracle.gemm(fmt, X, W, N, R=R)
+    tolerance.check(host(Yr), refr, tolerance.gemm_bound(refr, axw, K))
+    refh = oracle.gemm(fmt, X, W, N, head_D=D)
+    tolerance.check(host(Yh), refh, tolerance.gemm_bound(refh, axw.reshape(M, H, D).transpose(1, 0, 2), K))
 
 
 # --------------------------------------------------------------------------

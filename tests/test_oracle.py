@@ -323,3 +323,132 @@ def test_layer_composes_pinned_pieces(oracle):
     np.testing.assert_array_equal(it["S"], oracle.swiglu(0, it["Xmid"], Ws[4], Ws[5], Nm))
     np.testing.assert_array_equal(out, oracle.gemm(0, it["S"], Ws[6], dm, R=it["Xmid"]))
     assert rng is not None
+
+
+# --------------------------------------------------------------------------
+# VAR_RATE_AFFINE, EXL3, PRISM_Q2_0, Q8_0 weights
+# --------------------------------------------------------------------------
+
+def _var_closed_form(blk_flat, codes, N, K):
+    """Closed form of cpu_gold_reference.h:225-320 from the DRAWN codes (stream
+    order j) and the header fields, permutation applied as the gold's dest_idx."""
+    b = blk_flat.reshape(N, K // 256, 160)
+    d = b[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    bias = b[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    w = np.zeros((N, K // 256, 8, 32))
+    for s in range(8):
+        S = d * b[..., 4 + s].astype(np.float64) * 0.0625
+        B = bias + d * (b[..., 12 + s].astype(np.float64) - 128.0) * 0.0625
+        mode = b[..., 20 + s]
+        depth, order = mode & 7, (mode >> 3) & 3
+        zero = np.where(depth == 3, 4.0, np.where(depth == 5, 16.0, 8.0))
+        for j in range(32):
+            u = (codes[:, :, s, j].astype(np.float64) - zero) * S + B
+            dst = np.where(order == 1, ((j & 1) << 4) | (j >> 1), np.where(order == 2, 31 - j, j))
+            np.put_along_axis(w[:, :, s], dst[..., None], u[..., None], axis=-1)
+    return w.reshape(N, K)
+
+
+def test_var_rate_generator_packing_agrees_with_gold_unpacking(oracle):
+    """synth restates the reference generator (bench_universal_router.mm:105-158,
+    3/5-bit codes as LSB-first streams, 4-bit as nibble pairs); the oracle
+    restates the gold's unpacking (cpu_gold_reference.h:233-320).  Every drawn
+    code must come back at its permuted position (orders 0, 1, 2)."""
+    N, K = 6, 512
+    got = {}
+    W = synth.var_rate_blocks(N, K, 11, got)
+    np.testing.assert_array_equal(oracle.dequantize_f64(4, W, K, N), _var_closed_form(W, got["codes"], N, K))
+
+
+def test_var_rate_order_probe(oracle):
+    """One nonzero code at stream position j lands on element dest(j):
+    order 1 interleaves (even j -> j/2, odd j -> 16 + j/2), order 2 reverses."""
+    for order in (0, 1, 2, 3):
+        for j in (0, 1, 2, 15, 16, 17, 30, 31):
+            blk = np.zeros(160, np.uint8)
+            blk[0:2] = _f16(16.0)                      # d: S = 16 * 16 / 16 = 16
+            blk[4] = 16
+            blk[12] = 128                              # B = 0
+            blk[20] = (order << 3) | 4                 # sub-block 0: 4-bit
+            codes = np.full(32, 8, np.uint8)           # code 8 -> weight 0
+            codes[j] = 9                               # -> weight S = 16
+            blk[32:48] = synth._pack_nibbles32(codes)
+            w = oracle.dequantize_f64(4, blk, 256, 1)[0][:32]
+            dest = {1: ((j & 1) << 4) | (j >> 1), 2: 31 - j}.get(order, j)
+            exp = np.zeros(32)
+            exp[dest] = 16.0
+            np.testing.assert_array_equal(w, exp)
+
+
+def test_var_rate_depth_and_offsets(oracle):
+    """Mode depth decides the zero point (4, 8, 16) and the payload width; the
+    payload of sub-block s starts at byte 32 + {0,12,24,40,56,72,88,108}[s]."""
+    for s in range(8):
+        for depth, width, zero in ((3, 12, 4), (4, 16, 8), (5, 20, 16)):
+            if synth.VAR_OFFSETS[s] + width > 128:
+                continue
+            blk = np.zeros(160, np.uint8)
+            blk[0:2] = _f16(16.0)
+            blk[4 + s] = 16
+            blk[12 + s] = 128
+            blk[20 + s] = depth
+            codes = np.arange(32) % (1 << depth)
+            off = 32 + synth.VAR_OFFSETS[s]
+            if depth == 4:
+                blk[off:off + 16] = synth._pack_nibbles32(codes)
+            else:
+                blk[off:off + width] = synth._pack_stream(codes.reshape(4, 8), depth).reshape(-1)
+            w = oracle.dequantize_f64(4, blk, 256, 1)[0][32 * s:32 * s + 32]
+            np.testing.assert_array_equal(w, (codes - zero) * 16.0)
+
+
+def test_exl3_generator_packing_agrees_with_gold_unpacking(oracle):
+    """synth restates the reference generator (bench_universal_router.mm:160-193);
+    the oracle the gold (cpu_gold_reference.h:345-392): w = (bias + S cb[q]) +
+    R cb[q + 8] for every drawn 3-bit code."""
+    N, K = 5, 512
+    got = {}
+    W = synth.exl3_blocks(N, K, 12, got)
+    b = W.reshape(N, K // 256, 144)
+    d = b[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    bias = b[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    cb = b[..., 20:36].copy().view(np.int8).astype(np.float64)
+    exp = np.zeros((N, K // 256, 8, 32))
+    for s in range(8):
+        S = d * b[..., 4 + s] * 0.015625
+        R = d * (b[..., 12 + s].astype(np.float64) - 128.0) * 0.0078125
+        q = got["codes"][:, :, s].astype(np.int64)
+        cbb = np.take_along_axis(cb, q, axis=-1)
+        cbr = np.take_along_axis(cb, q + 8, axis=-1)
+        exp[:, :, s] = bias[..., None] + S[..., None] * cbb + R[..., None] * cbr
+    np.testing.assert_array_equal(oracle.dequantize_f64(5, W, K, N), exp.reshape(N, K))
+    # the generator's codebook: (c - 3.5) * 8 and (c - 3.5) * 3 truncated toward zero
+    np.testing.assert_array_equal(cb[0, 0], [-28, -20, -12, -4, 4, 12, 20, 28, -10, -7, -4, -1, 1, 4, 7, 10])
+
+
+def test_prism_layout_probe(oracle):
+    """Code c at bits 2j of byte i is element 4i + j (cpu_gold_reference.h:
+    418-426); the Metal unpacker reads the same element as bits 2(e % 16) of
+    little-endian word e / 16 of the sub-block (quant_router_kernels.metal:414-436)."""
+    for e in (0, 1, 3, 4, 15, 16, 31, 64, 127):
+        for c, val in ((0, -1.0), (2, 1.0), (3, 2.0)):
+            blk = np.zeros(34, np.uint8)
+            blk[0:2] = _f16(0.5)
+            words = np.full(8, 0x55555555, np.uint32)   # every code 1 -> weight 0
+            sub, r = divmod(e, 32)
+            wi, bit = sub * 2 + r // 16, 2 * (r % 16)
+            words[wi] = (words[wi] & ~np.uint32(3 << bit)) | np.uint32(c << bit)
+            blk[2:] = words.view(np.uint8)
+            w = oracle.dequantize_f64(7, blk, 128, 1)[0]
+            exp = np.zeros(128)
+            exp[e] = val * 0.5
+            np.testing.assert_array_equal(w, exp)
+
+
+def test_q8_0_weights_match_kv_dequantizer(oracle):
+    """The Q8_0 weight decoder equals the Q8_0 KV dequantizer pinned above
+    (same 34-byte block, w = q d)."""
+    x = (np.random.default_rng(3).standard_normal(64 * 32) * 3).astype(np.float16)
+    q = oracle.quantize_q8_0(x)
+    np.testing.assert_array_equal(oracle.dequantize(6, q, 64 * 32, 1).reshape(-1).view(np.uint16),
+                                  oracle.dequantize_q8_0(q).reshape(-1).view(np.uint16))
