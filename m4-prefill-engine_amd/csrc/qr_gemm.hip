@@ -293,6 +293,8 @@ gemm_rb_kernel(GemmParams p) {
         static_assert(NP % BATCH == 0 && BATCH % 8 == 0, "whole 32x32 tiles per batch");
         const uint32_t T = nt_m * nt_n;
         const uint32_t tile = tmi * nt_n + tni;
+        // tile row of accumulator element r of tile i (the pair r, r + 1 covers it and the next row)
+        auto pair_row = [&](int i, int r) { return 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
         auto pair_ptr = [&](uint32_t z) {
             return reinterpret_cast<uint64_t*>(p.ws) + ((size_t)z * T + tile) * (NP * NT) + tid;
         };
@@ -306,7 +308,8 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
                     for (int r = 0; r < 16; r += 2, q++) {
                         const uint64_t v = (uint64_t)f32_bits(acc[i][j][r]) | ((uint64_t)f32_bits(acc[i][j][r + 1]) << 32);
-                        __hip_atomic_store(dst + q * NT, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (pair_row(i, r) < mrows)  // rows past M are never written out
+                            __hip_atomic_store(dst + q * NT, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
@@ -319,28 +322,45 @@ gemm_rb_kernel(GemmParams p) {
         }
         __syncthreads();
         if (!s_last) return;
-        // sum all splits in split order (deterministic)
+        // sum all splits in split order (deterministic); this workgroup's own
+        // split comes from its registers, the others from the workspace
+        f16v_t tot[TM][NCB];
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < NCB; j++) acc[i][j] = f16v_t{};
+            for (int j = 0; j < NCB; j++) tot[i][j] = f16v_t{};
         for (uint32_t z = 0; z < ksplit; z++) {
+            if (z == kz) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < NCB; j++) tot[i][j] += acc[i][j];
+                continue;
+            }
             const uint64_t* src = pair_ptr(z);
 #pragma unroll
             for (int q0 = 0; q0 < NP; q0 += BATCH) {
                 uint64_t t[BATCH];
 #pragma unroll
-                for (int q = 0; q < BATCH; q++)
-                    t[q] = __hip_atomic_load(src + (q0 + q) * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int q = 0; q < BATCH; q++) {
+                    const int qq = q0 + q;
+                    t[q] = pair_row((qq / 8) / NCB, 2 * (qq % 8)) < mrows
+                               ? __hip_atomic_load(src + qq * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : 0ull;
+                }
 #pragma unroll
                 for (int q = 0; q < BATCH; q++) {
                     const int qq = q0 + q;               // pair index: tile qq / 8, rows 2 (qq % 8)
                     const int i = (qq / 8) / NCB, j = (qq / 8) % NCB, r = 2 * (qq % 8);
-                    acc[i][j][r] += bits_f32((uint32_t)t[q]);
-                    acc[i][j][r + 1] += bits_f32((uint32_t)(t[q] >> 32));
+                    tot[i][j][r] += bits_f32((uint32_t)t[q]);
+                    tot[i][j][r + 1] += bits_f32((uint32_t)(t[q] >> 32));
                 }
             }
         }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < NCB; j++) acc[i][j] = tot[i][j];
         if (tid == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
