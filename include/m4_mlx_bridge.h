@@ -78,9 +78,20 @@ M4_API int m4_bridge_validate_gemm(const void* X_ptr, size_t X_bytes, const void
                             const void* Y_ptr, size_t Y_bytes, int format, uint32_t M, uint32_t K,
                             uint32_t N);
 
+/* Projection for every format with a kernel: formats 0..5 as
+ * m4_bridge_dispatch_gemm, plus PRISM_Q2_0 (7; K % 128 == 0) and Q8_0 weights
+ * (6).  Replaces the registry's kernels reached by name,
+ * quant_router_gemm_<fmt>_64x64 (quant_router_kernels.metal:588-750,
+ * prism_q2_0 at :726; names from src/router/quant_registry.mm:60-172 --
+ * quant_router_gemm_q8_0_64x64 is named there but has no Metal kernel).
+ * Same validation order and codes as dispatch_gemm with the wider format set. */
+M4_API int m4_bridge_dispatch_router_gemm(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes, void* Y_ptr,
+                                   size_t Y_bytes, int format, uint32_t M, uint32_t K, uint32_t N);
+
 /* Direct-head projection: Y is [H, M, D] with N = H * D; replaces
  * quant_router_head_gemm_<fmt>_64x64 (quant_router_kernels.metal:754-927,
- * index map :570-574).  Same validation as dispatch_gemm with N = H * D. */
+ * index map :570-574).  Same validation as dispatch_router_gemm with N = H * D
+ * (formats 0..7). */
 M4_API int m4_bridge_dispatch_head_gemm(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes, void* Y_ptr,
                                  size_t Y_bytes, int format, uint32_t M, uint32_t H, uint32_t D,
                                  uint32_t K);
@@ -94,7 +105,7 @@ M4_API int m4_bridge_dispatch_gemm_residual(void* X_ptr, size_t X_bytes, void* W
 
 /* Fused dual-projection SwiGLU: Out[M, N_mlp] = silu(X . Wg^T) * (X . Wu^T);
  * replaces swiglu_mma_dual_simd (brick3_swiglu_kernels.metal:428-698), which
- * takes Q4_0 only; any projection format 0..3 is accepted here. */
+ * takes Q4_0 only; any format with kernels (0..7) is accepted here. */
 M4_API int m4_bridge_dispatch_swiglu(void* X_ptr, size_t X_bytes, void* Wg_ptr, size_t Wg_bytes, void* Wu_ptr,
                               size_t Wu_bytes, void* Out_ptr, size_t Out_bytes, int format, uint32_t M,
                               uint32_t N_mlp, uint32_t K);
@@ -126,7 +137,7 @@ M4_API int m4_bridge_prefill_layer(void* X_ptr, void* Wq, void* Wk, void* Wv, vo
                             uint32_t D, uint32_t N_mlp, float attn_scale);
 
 /* Dequantize W [N, K] to fp16 [N, K] with the kernels' own decoders (the
- * registry's dequantize hook, src/router/quant_registry.h:24). Formats 0..3. */
+ * registry's dequantize hook, src/router/quant_registry.h:24). Formats 0..7. */
 M4_API int m4_bridge_dequantize(void* W_ptr, size_t W_bytes, void* out_ptr, size_t out_bytes, int format,
                          uint32_t K, uint32_t N);
 

@@ -117,19 +117,24 @@ void sync_and_release() {
     g_staged_bytes = 0;
 }
 
+// Formats m4_bridge_dispatch_gemm accepts (m4_mlx_bridge.mm:28-35, 211), and
+// the wider set the kernel-name entry points accept: every format with a
+// kernel here, i.e. also Q8_0 weights (6) and PRISM_Q2_0 (7).
 bool is_projection_format(int f) { return f >= 0 && f < 6; }
-bool has_kernels(int f) { return f >= 0 && f < 6; }
+bool has_kernels(int f) { return f >= 0 && f < 8; }
 
-// core/bridge/m4_mlx_bridge.mm:204-230, minus the init check.
+// core/bridge/m4_mlx_bridge.mm:204-230, minus the init check.  `ext` widens
+// the format range to every format with kernels (PRISM_Q2_0 needs K % 128).
 int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, size_t Yb, int format,
-             uint32_t M, uint32_t K, uint32_t N) {
+             uint32_t M, uint32_t K, uint32_t N, bool ext = false) {
     if (!X || !W || !Y) return -2;
     if ((reinterpret_cast<uintptr_t>(X) % 2) || (reinterpret_cast<uintptr_t>(Y) % 2)) return -2;
-    if (!is_projection_format(format)) return -3;
+    if (!(ext ? has_kernels(format) : is_projection_format(format))) return -3;
     if (M == 0 || K == 0 || N == 0) return -4;
     if (K % 32) return -4;
     if ((format == 2 || format == 4 || format == 5) && (K % 256)) return -4;
-    if (Xb < (size_t)M * K * 2 || Yb < (size_t)M * N * 2 || Wb < qr::expected_weight_bytes(format, K, N))
+    if (format == 7 && (K % 128)) return -4;
+    if (Xb < (size_t)M * K * 2 || Yb < (size_t)M * N * 2 || Wb < qr::kernel_weight_bytes(format, K, N))
         return -2;
     return 0;
 }
@@ -207,12 +212,12 @@ int launch(const qr::GemmParams& p0) {
 }
 
 int gemm_common(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, void* R, int format, uint32_t M,
-                uint32_t K, uint32_t N, uint32_t head_D) {
+                uint32_t K, uint32_t N, uint32_t head_D, bool ext) {
     if (!g_initialized) return -1;
-    int rc = validate(X, Xb, W, Wb, Y, Yb, format, M, K, N);
+    int rc = validate(X, Xb, W, Wb, Y, Yb, format, M, K, N, ext);
     if (rc) return rc;
     if (!has_kernels(format)) return -3;
-    const size_t wbytes = qr::expected_weight_bytes(format, K, N);
+    const size_t wbytes = qr::kernel_weight_bytes(format, K, N);
     std::lock_guard<std::mutex> lk(g_mu);
     void* dx = resolve(X, (size_t)M * K * 2, 16, true, false);
     void* dw = resolve(W, wbytes, 16, true, false);
@@ -270,7 +275,12 @@ int m4_bridge_validate_gemm(const void* X, size_t Xb, const void* W, size_t Wb, 
 
 int m4_bridge_dispatch_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format, uint32_t M,
                             uint32_t K, uint32_t N) {
-    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, N, 0);
+    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, N, 0, false);
+}
+
+int m4_bridge_dispatch_router_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format,
+                                   uint32_t M, uint32_t K, uint32_t N) {
+    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, N, 0, true);
 }
 
 int m4_bridge_dispatch_gemv(void* x, size_t xb, void* W, size_t Wb, void* y, size_t yb, int format, uint32_t K,
@@ -282,7 +292,7 @@ int m4_bridge_dispatch_head_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y
                                  uint32_t H, uint32_t D, uint32_t K) {
     if (!g_initialized) return -1;
     if (H == 0 || D == 0) return -4;
-    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, H * D, D);
+    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, H * D, D, true);
 }
 
 int m4_bridge_dispatch_gemm_residual(void* X, size_t Xb, void* W, size_t Wb, void* R, size_t Rb, void* Y, size_t Yb,
@@ -290,18 +300,17 @@ int m4_bridge_dispatch_gemm_residual(void* X, size_t Xb, void* W, size_t Wb, voi
     if (!g_initialized) return -1;
     if (!R || (reinterpret_cast<uintptr_t>(R) % 2)) return -2;
     if (Rb < (size_t)M * N * 2) return -2;
-    return gemm_common(X, Xb, W, Wb, Y, Yb, R, format, M, K, N, 0);
+    return gemm_common(X, Xb, W, Wb, Y, Yb, R, format, M, K, N, 0, true);
 }
 
 int m4_bridge_dispatch_swiglu(void* X, size_t Xb, void* Wg, size_t Wgb, void* Wu, size_t Wub, void* Out,
                               size_t Outb, int format, uint32_t M, uint32_t Nm, uint32_t K) {
     if (!g_initialized) return -1;
-    int rc = validate(X, Xb, Wg, Wgb, Out, Outb, format, M, K, Nm);
+    int rc = validate(X, Xb, Wg, Wgb, Out, Outb, format, M, K, Nm, true);
     if (rc) return rc;
     if (!Wu) return -2;
-    if (Wub < qr::expected_weight_bytes(format, K, Nm)) return -2;
-    if (!has_kernels(format)) return -3;
-    const size_t wbytes = qr::expected_weight_bytes(format, K, Nm);
+    if (Wub < qr::kernel_weight_bytes(format, K, Nm)) return -2;
+    const size_t wbytes = qr::kernel_weight_bytes(format, K, Nm);
     std::lock_guard<std::mutex> lk(g_mu);
     void* dx = resolve(X, (size_t)M * K * 2, 16, true, false);
     void* dg = resolve(Wg, wbytes, 16, true, false);
@@ -371,11 +380,11 @@ int m4_bridge_dispatch_flash_attn_q8_0(void* Q, size_t Qb, void* Kq, size_t Kqb,
 int m4_bridge_dequantize(void* W, size_t Wb, void* out, size_t outb, int format, uint32_t K, uint32_t N) {
     if (!g_initialized) return -1;
     if (!W || !out) return -2;
-    if (!is_projection_format(format)) return -3;
-    if (K == 0 || N == 0 || K % 32) return -4;
-    if (format == 2 && K % 256) return -4;
     if (!has_kernels(format)) return -3;
-    const size_t wbytes = qr::expected_weight_bytes(format, K, N);
+    if (K == 0 || N == 0 || K % 32) return -4;
+    if ((format == 2 || format == 4 || format == 5) && K % 256) return -4;
+    if (format == 7 && K % 128) return -4;
+    const size_t wbytes = qr::kernel_weight_bytes(format, K, N);
     if (Wb < wbytes || outb < (size_t)N * K * 2) return -2;
     if (wbytes >= (1ull << 31)) return -4;
     std::lock_guard<std::mutex> lk(g_mu);
@@ -449,7 +458,7 @@ int m4_bridge_prefill_layer(void* X, void* Wq, void* Wk, void* Wv, void* Wo, voi
         p.R = R;
         p.M = M; p.N = N; p.K = Kd;
         p.head_D = headD;
-        p.col_bytes = qr::expected_weight_bytes(format, Kd, N) / N;
+        p.col_bytes = qr::kernel_weight_bytes(format, Kd, N) / N;
         return launch(p);
     };
     int rc = 0;

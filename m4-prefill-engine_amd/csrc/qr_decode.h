@@ -194,6 +194,27 @@ template <> struct Decoder<QUANT_Q4_K> {
     __device__ static uint32_t parity(uint32_t, uint32_t kb) { return kb & 7u; }
 };
 
+// 16 two-bit codes of word q (element e at bits 2e, LSB first) as 8 binary16
+// pairs (c - 1) d: 1024 + c - 1025 is exact, and so is the product (c - 1) d
+// for c in 0..3 (code 3 gives +2d).  Shared by TERNARY_1_58 and PRISM_Q2_0.
+__device__ __forceinline__ void two_bit_word(uint32_t q, uint32_t d16, uint32_t out[8]) {
+    const h2_t d = as_h2(d16 | (d16 << 16));
+    const h2_t off = {(_Float16)1025.0f, (_Float16)1025.0f};
+    const uint32_t ev = q & 0x33333333u;         // codes of even elements, one per nibble
+    const uint32_t od = (q >> 2) & 0x33333333u;  // codes of odd elements
+    const uint32_t ev_lo = ev & 0x0f0f0f0fu, ev_hi = (ev >> 4) & 0x0f0f0f0fu;
+    const uint32_t od_lo = od & 0x0f0f0f0fu, od_hi = (od >> 4) & 0x0f0f0f0fu;
+    // nibble j (elements 2j, 2j+1): j even -> byte j/2 of *_lo, j odd -> of *_hi
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)(b + 4) << 16);
+        const uint32_t p0 = perm(od_lo, ev_lo, sel) | 0x64006400u;  // nibble 2b
+        const uint32_t p1 = perm(od_hi, ev_hi, sel) | 0x64006400u;  // nibble 2b+1
+        out[2 * b + 0] = as_u32((as_h2(p0) - off) * d);
+        out[2 * b + 1] = as_u32((as_h2(p1) - off) * d);
+    }
+}
+
 // --------------------------------------------------------------------------
 // TERNARY_1_58: 12-byte blocks (dword aligned); qs[0] holds elements 0..15,
 // qs[1] elements 16..31, two bits each, LSB first.  w = (1024 + c - 1025) * d
@@ -209,23 +230,7 @@ template <> struct Decoder<QUANT_TERNARY_1_58> {
         for (int i = 0; i < 3; i++) raw[i] = ld_b32(r, o + 4u * i);
     }
     __device__ static void decode_half(const uint32_t raw[3], uint32_t, int h, uint32_t out[8]) {
-        const uint32_t d16 = raw[0] & 0xffffu;
-        const h2_t d = as_h2(d16 | (d16 << 16));
-        const h2_t off = {(_Float16)1025.0f, (_Float16)1025.0f};
-        const uint32_t q = h ? raw[2] : raw[1];
-        const uint32_t ev = q & 0x33333333u;         // codes of even elements, one per nibble
-        const uint32_t od = (q >> 2) & 0x33333333u;  // codes of odd elements
-        const uint32_t ev_lo = ev & 0x0f0f0f0fu, ev_hi = (ev >> 4) & 0x0f0f0f0fu;
-        const uint32_t od_lo = od & 0x0f0f0f0fu, od_hi = (od >> 4) & 0x0f0f0f0fu;
-        // nibble j (elements 2j, 2j+1): j even -> byte j/2 of *_lo, j odd -> of *_hi
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)(b + 4) << 16);
-            const uint32_t p0 = perm(od_lo, ev_lo, sel) | 0x64006400u;  // nibble 2b
-            const uint32_t p1 = perm(od_hi, ev_hi, sel) | 0x64006400u;  // nibble 2b+1
-            out[2 * b + 0] = as_u32((as_h2(p0) - off) * d);
-            out[2 * b + 1] = as_u32((as_h2(p1) - off) * d);
-        }
+        two_bit_word(h ? raw[2] : raw[1], raw[0] & 0xffffu, out);
     }
     __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
 };
@@ -365,6 +370,73 @@ template <> struct Decoder<QUANT_EXL3> {
         }
     }
     __device__ static uint32_t parity(uint32_t, uint32_t kb) { return kb & 7u; }
+};
+
+// --------------------------------------------------------------------------
+// PRISM_Q2_0: 34-byte blocks of 128 elements {f16 d; u8 qs[32]}, four 2-bit
+// codes per byte LSB first, element 4 i + j at bits 2 j of qs[i]
+// (cpu_gold_reference.h:418-430; quant_router_kernels.metal:414-436).  Group
+// kb is sub-block s = kb % 4 of block kb / 4: code bytes 8 s .. 8 s + 7, the
+// same bit order as a ternary code word, so w = (c - 1) d with code 3 -> +2d
+// (the gold and the reference's PRISM kernel agree on it).  Blocks are only
+// 2-byte aligned: three aligned dwords cover the 8 code bytes at either
+// parity, plus the dword holding d.  parity() packs the block's byte parity
+// (bit 1) and s (bits 2..3).
+// --------------------------------------------------------------------------
+template <> struct Decoder<QUANT_PRISM_Q2_0> {
+    static constexpr int kBlockElems = 32;   // decode granularity (sub-block)
+    static constexpr int kBlockBytes = 34;   // per 128 elements
+    static constexpr int kRawWords = 4;
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[4]) {
+        const uint32_t b = col_off + (kb >> 2) * 34u;
+        const uint32_t c = (b + 2u + 8u * (kb & 3u)) & ~3u;
+        raw[0] = ld_b32(r, b & ~3u);
+        raw[1] = ld_b32(r, c);
+        raw[2] = ld_b32(r, c + 4u);
+        raw[3] = ld_b32(r, c + 8u);
+    }
+    __device__ static void decode_half(const uint32_t raw[4], uint32_t par, int h, uint32_t out[8]) {
+        // block at byte 0 of its dword: d low, codes start at byte 2 of raw[1]
+        const bool lo = (par & 2u) == 0;
+        const uint32_t d16 = lo ? (raw[0] & 0xffffu) : (raw[0] >> 16);
+        const uint32_t q = lo ? __builtin_amdgcn_alignbyte(raw[2 + h], raw[1 + h], 2) : raw[1 + h];
+        two_bit_word(q, d16, out);
+    }
+    __device__ static uint32_t parity(uint32_t col_off, uint32_t kb) {
+        return ((col_off + (kb >> 2) * 34u) & 2u) | ((kb & 3u) << 2);
+    }
+};
+
+// --------------------------------------------------------------------------
+// Q8_0 weights: 34-byte blocks {f16 d; i8 qs[32]}, w = q d (the registry's
+// quant_router_gemm_q8_0_64x64, quant_registry.mm:153, a kernel the reference
+// never wrote; the block is the KV-cache block of brick4_attn_bench.mm:57-65).
+// q is exact in binary16 (magic exponent: 1024 + (q + 128) - 1152) and the
+// product rounds once.  Nine aligned dwords cover the block at either parity.
+// --------------------------------------------------------------------------
+template <> struct Decoder<QUANT_Q8_0> {
+    static constexpr int kBlockElems = 32;
+    static constexpr int kBlockBytes = 34;
+    static constexpr int kRawWords = 9;
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[9]) {
+        const uint32_t a = (col_off + kb * 34u) & ~3u;
+#pragma unroll
+        for (int i = 0; i < 9; i++) raw[i] = ld_b32(r, a + 4u * i);
+    }
+    __device__ static void decode_half(const uint32_t raw[9], uint32_t par, int h, uint32_t out[8]) {
+        const bool lo = par == 0u;  // block at byte 0 of raw[0]: codes from byte 2
+        const uint32_t d16 = lo ? (raw[0] & 0xffffu) : (raw[0] >> 16);
+        const h2_t d = as_h2(d16 | (d16 << 16));
+        const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int w = 4 * h + i;  // code word: elements 4w .. 4w + 3
+            const uint32_t q = (lo ? __builtin_amdgcn_alignbyte(raw[w + 1], raw[w], 2) : raw[w + 1]) ^ 0x80808080u;
+            out[2 * i + 0] = as_u32((as_h2(nib_pair_lo(q)) - off) * d);
+            out[2 * i + 1] = as_u32((as_h2(nib_pair_hi(q)) - off) * d);
+        }
+    }
+    __device__ static uint32_t parity(uint32_t col_off, uint32_t kb) { return (col_off + kb * 34u) & 2u; }
 };
 
 // Branch-free half-group decode for pipelined callers: bit-exact whenever no

@@ -97,4 +97,16 @@ inline size_t expected_weight_bytes(int format, uint32_t K, uint32_t N) {
     }
 }
 
+// W bytes the kernels read for every format that has kernels here: formats
+// 0..5 as above, plus Q8_0 weights (34 B / 32) and PRISM_Q2_0 (34 B / 128),
+// which the reference reaches only through its kernel names
+// (quant_router_kernels.metal:726, :904; quant_registry.mm:153).
+inline size_t kernel_weight_bytes(int format, uint32_t K, uint32_t N) {
+    switch (format) {
+        case QUANT_Q8_0: return ((size_t)K / 32) * N * 34;
+        case QUANT_PRISM_Q2_0: return ((size_t)K / 128) * N * 34;
+        default: return expected_weight_bytes(format, K, N);
+    }
+}
+
 }  // namespace qr

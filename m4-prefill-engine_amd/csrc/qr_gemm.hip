@@ -47,6 +47,9 @@ namespace qr {
 #ifndef QR_RB_VPM
 #define QR_RB_VPM 5
 #endif
+#ifndef QR_RB_ADIST
+#define QR_RB_ADIST 1
+#endif
 
 
 namespace rb {
@@ -198,7 +201,11 @@ gemm_rb_kernel(GemmParams p) {
     };
 
     uint32_t bw[2][NCB][16];
-    h8_t af[2][TM];
+    // A fragments are read AD slices ahead of the MFMAs that use them (ring of
+    // AD + 1 slots; slice t = 4 j + kk of the unrolled group uses slot t % (AD + 1)).
+    constexpr int AD = QR_RB_ADIST;
+    static_assert((4 * U) % (AD + 1) == 0, "A ring divides the unrolled slices");
+    h8_t af[AD + 1][TM];
 
     // One K step, as four k-slices.  Slice kk: read the A fragments of slice
     // kk + 1 (of step s + 1 for the last slice), the TM x NCB MFMAs of slice kk,
@@ -216,15 +223,16 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             __builtin_amdgcn_sched_barrier(0);
-            if (kk < 3) read_a(j % XS, kk + 1, af[(kk + 1) & 1]);
-            else read_a((j + 1) % XS, 0, af[0]);
+            const int t = 4 * j + kk;
+            if (kk + AD < 4) read_a(j % XS, kk + AD, af[(t + AD) % (AD + 1)]);
+            else read_a((j + 1) % XS, kk + AD - 4, af[(t + AD) % (AD + 1)]);
 #pragma unroll
             for (int jb = 0; jb < NCB; jb++) {
                 const uint32_t* bj = bw[j & 1][jb];
                 const h8_t b = __builtin_bit_cast(h8_t, u4_t{bj[4 * kk], bj[4 * kk + 1], bj[4 * kk + 2], bj[4 * kk + 3]});
 #pragma unroll
                 for (int i = 0; i < TM; i++)
-                    acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], b, acc[i][jb], 0, 0, 0);
+                    acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t % (AD + 1)][i], b, acc[i][jb], 0, 0, 0);
             }
             if (kk < HALVES) {
                 const int jb = kk >> 1, hh = kk & 1;
@@ -268,7 +276,8 @@ gemm_rb_kernel(GemmParams p) {
     decode(0, 0, bw[0]);
     load_w(WP, 0);
     __syncthreads();
-    read_a(0, 0, af[0]);
+#pragma unroll
+    for (int t = 0; t < AD; t++) read_a(0, t, af[t]);
 
     // ---- main loop: full groups of U steps branch-free (look-ahead fetches past
     // the K range read zeros), then the remainder with guards ----
@@ -530,6 +539,8 @@ hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
         case QUANT_TERNARY_1_58: return dual ? rb_launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : rb_launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
         case QUANT_VAR_RATE_AFFINE: return dual ? rb_launch_fmt<QUANT_VAR_RATE_AFFINE, true>(p, st) : rb_launch_fmt<QUANT_VAR_RATE_AFFINE, false>(p, st);
         case QUANT_EXL3: return dual ? rb_launch_fmt<QUANT_EXL3, true>(p, st) : rb_launch_fmt<QUANT_EXL3, false>(p, st);
+        case QUANT_Q8_0: return dual ? rb_launch_fmt<QUANT_Q8_0, true>(p, st) : rb_launch_fmt<QUANT_Q8_0, false>(p, st);
+        case QUANT_PRISM_Q2_0: return dual ? rb_launch_fmt<QUANT_PRISM_Q2_0, true>(p, st) : rb_launch_fmt<QUANT_PRISM_Q2_0, false>(p, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -62,6 +62,7 @@ SIGNATURES = {
     "m4_bridge_is_initialized": ([], ctypes.c_bool),
     "m4_bridge_shutdown": ([], None),
     "m4_bridge_validate_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
+    "m4_bridge_dispatch_router_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_head_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_gemm_residual": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_swiglu": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
@@ -246,6 +247,24 @@ class HIPBridge:
         self._lib.m4_bridge_shutdown()
 
     # -- router extensions ----------------------------------------------------
+    def dispatch_router_gemm(self, X, W, Y, format, M=None, K=None, N=None, check_finite: bool = False) -> int:
+        """Y = X . W^T for every format with a kernel, PRISM_Q2_0 and Q8_0 weights
+        included (quant_router_gemm_<fmt>_64x64, quant_router_kernels.metal:588-750)."""
+        x_ptr, x_bytes = self.extract_buffer_address_and_size(X)
+        w_ptr, w_bytes = self.extract_buffer_address_and_size(W)
+        y_ptr, y_bytes = self.extract_buffer_address_and_size(Y)
+        M = X.shape[0] if M is None else M
+        K = X.shape[1] if K is None else K
+        N = Y.shape[1] if N is None else N
+        self._bind_stream(X, W, Y)
+        ret = self._lib.m4_bridge_dispatch_router_gemm(x_ptr, x_bytes, w_ptr, w_bytes, y_ptr, y_bytes, int(format),
+                                                       int(M), int(K), int(N))
+        self._check("m4_bridge_dispatch_router_gemm", ret)
+        self._in_flight_tensors.append((X, W, Y))
+        if check_finite:
+            self._pending_finite_checks.append(Y)
+        return ret
+
     def dispatch_head_gemm(self, X, W, Y, format, M, H, D, K, check_finite: bool = False) -> int:
         """Direct-head projection: Y [H, M, D] (quant_router_kernels.metal:754-927)."""
         a = [self.extract_buffer_address_and_size(t) for t in (X, W, Y)]

@@ -20,6 +20,7 @@ from __future__ import annotations
 import numpy as np
 
 Q4_0, MLX_4BIT, Q4_K, TERNARY_1_58, VAR_RATE_AFFINE, EXL3 = 0, 1, 2, 3, 4, 5
+Q8_0, PRISM_Q2_0 = 6, 7
 BLOCK_ELEMS = {0: 32, 1: 32, 2: 256, 3: 32, 4: 256, 5: 256, 6: 32, 7: 128}
 BLOCK_BYTES = {0: 18, 1: 20, 2: 144, 3: 12, 4: 160, 5: 144, 6: 34, 7: 34}
 
@@ -222,6 +223,17 @@ def random_blocks(fmt: int, N: int, K: int, seed: int, code3: bool = False) -> n
         return var_rate_blocks(N, K, seed)
     elif fmt == EXL3:
         return exl3_blocks(N, K, seed)
+    elif fmt == Q8_0:
+        # no reference generator for Q8_0 weights: every int8 code, small scales
+        out = np.empty((N, nb, 34), np.uint8)
+        out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.004 + 0.0005).astype(np.float32))
+        out[..., 2:] = rng.integers(0, 256, (N, nb, 32), dtype=np.uint8)
+    elif fmt == PRISM_Q2_0:
+        # tests/e2e/test_common.h:415-427: d in [0.01, 0.05), every 2-bit code
+        # 0..3 (code 3 included), four per byte LSB first
+        out = np.empty((N, nb, 34), np.uint8)
+        out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.04 + 0.01).astype(np.float32))
+        out[..., 2:] = rng.integers(0, 256, (N, nb, 32), dtype=np.uint8)
     else:
         raise ValueError(f"no random generator for format {fmt}")
     return out.reshape(-1)

@@ -125,6 +125,8 @@ def test_uninitialized_bridge_refuses_work(lib):
                                        0, 64, 128, 64) == -1
     assert lib.m4_bridge_dispatch_gemv(x.ctypes.data, 256, w.ctypes.data, w.nbytes, y.ctypes.data, 128,
                                        0, 128, 64) == -1
+    assert lib.m4_bridge_dispatch_router_gemm(x.ctypes.data, x.nbytes, w.ctypes.data, w.nbytes, y.ctypes.data,
+                                              y.nbytes, 7, 64, 128, 64) == -1
     lib.m4_bridge_synchronize()
     lib.m4_bridge_shutdown()
     assert lib.m4_bridge_get_uma_footprint_mb() > 0.0

@@ -54,14 +54,14 @@ def weights(kind, fmt, N, K, seed):
 # --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("fmt,K", [(0, 512), (0, 96), (1, 512), (1, 96), (2, 512), (3, 512), (3, 96), (4, 512),
-                                   (5, 512)])
+                                   (5, 512), (6, 512), (6, 96), (7, 512), (7, 384)])
 @pytest.mark.parametrize("kind", ["random", "quantized"])
 def test_dequant_bit_exact(bridge, oracle, fmt, K, kind):
     N = 72
     if kind == "quantized" and fmt == 1 and K % 64:
         pytest.skip("MLX g64 quantizer needs K % 64 == 0")
     if kind == "quantized" and fmt >= 4:
-        pytest.skip("VAR_RATE_AFFINE / EXL3 come from the reference's random generators only")
+        pytest.skip("formats 4..7 come from random generators only (no BASELINE quantizer)")
     W = weights(kind, fmt, N, K, 100 + fmt)
     out = empty16(N, K)
     bridge.dequantize(dev(W), out, fmt, K, N)
@@ -123,6 +123,38 @@ def test_gemm_var_rate_and_exl3(bridge, oracle, fmt, M, K, N):
     H, D = N // 64, 64
     Yh = empty16(H, M, D)
     bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    bridge.synchronize()
+    axw = absxw(oracle, fmt, X, W, K, N)
+    ref = oracle.gemm(fmt, X, W, N)
+    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, axw, K))
+    refr = oracle.gemm(fmt, X, W, N, R=R)
+    tolerance.check(host(Yr), refr, tolerance.gemm_bound(refr, axw, K))
+    refh = oracle.gemm(fmt, X, W, N, head_D=D)
+    tolerance.check(host(Yh), refh, tolerance.gemm_bound(refh, axw.reshape(M, H, D).transpose(1, 0, 2), K))
+
+
+@pytest.mark.parametrize("fmt", [6, 7])
+@pytest.mark.parametrize("M,K,N", [(1, 384, 256), (33, 384, 200), (129, 512, 256), (128, 4096, 320),
+                                   (300, 1152, 136)])
+def test_gemm_q8_0_and_prism(bridge, oracle, fmt, M, K, N):
+    """Q8_0 weights and PRISM_Q2_0 (code 3 = +2d included) through the
+    kernel-name entry point (quant_router_gemm_<fmt>_64x64) and the head and
+    residual entry points; K = 384 / 1152 give 2-byte-aligned columns
+    (34-byte blocks), 4096 a split-K launch; the plain dispatch_gemm keeps the
+    reference's format range and refuses them with -3."""
+    X = synth.activations(M, K, 90 + M, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 91 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    R = synth.activations(M, N, 92)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    D = 8 if N % 64 else 64
+    H = N // D
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    with pytest.raises(RuntimeError):
+        bridge.dispatch_gemm(dev(X), dev(W), empty16(M, N), fmt, M, K, N)
     bridge.synchronize()
     axw = absxw(oracle, fmt, X, W, K, N)
     ref = oracle.gemm(fmt, X, W, N)
