@@ -17,7 +17,11 @@ OUT = HERE / "libm4_bridge.so"
 BUILD = HERE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["qr_gemm.hip", "qr_gemm_skinny.hip", "qr_dequant.hip", "qr_attention.hip", "qr_bridge.cpp", "qr_registry.cpp"]
+# (source, object stem, extra defines).  The tiled projection kernel is built
+# once per format (0..7) so its instantiations compile in parallel.
+SOURCES = ([("qr_gemm.hip", f"qr_gemm_f{f}", (f"-DQR_GEMM_FORMAT={f}",)) for f in range(8)] +
+           [(s, s.rsplit(".", 1)[0], ()) for s in ("qr_gemm_host.hip", "qr_gemm_skinny.hip", "qr_dequant.hip",
+                                                   "qr_attention.hip", "qr_bridge.cpp", "qr_registry.cpp")])
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-ffp-contract=on",
           "-fvisibility=hidden", "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
@@ -27,18 +31,19 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-ffp-contract=
 DEVICE = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def _compile(src: str, build_dir: Path = BUILD, extra: tuple = ()) -> Path:
-    obj = build_dir / (Path(src).stem + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(unit: tuple, build_dir: Path = BUILD, extra: tuple = ()) -> Path:
+    src, stem, defs = unit
+    obj = build_dir / (stem + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE, *defs, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
-        cmd = [HIPCC, *COMMON, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *defs, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {src}\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     return obj
 
 
-def build(jobs: int = 4, verbose: bool = False, out: Path = OUT, build_dir: Path = BUILD,
+def build(jobs: int = 8, verbose: bool = False, out: Path = OUT, build_dir: Path = BUILD,
           extra: tuple = ()) -> Path:
     """Compile every source (optionally with extra compiler flags, e.g. -D
     tuning macros) and link `out`."""

@@ -1,5 +1,7 @@
 // qr_gemm.hip -- quantized projection Y = X . W^T on gfx950 MFMA, weights
 // decoded straight into MFMA B-operand registers (tiled, M > 64).
+// Built once per format with -DQR_GEMM_FORMAT=F (one kernel family per
+// compilation unit, so the formats compile in parallel).
 //
 // Replaces the reference's block_mma_64x64_engine (quant_router_kernels.metal:
 // 442-581) with its entry points (:588-927), and the fused dual-projection
@@ -37,7 +39,7 @@
 //    stores; the last workgroup of the tile (agent-scope counter) sums them in
 //    split order -- deterministic, one launch.
 #include "qr_decode.h"
-#include "qr_kernels.h"
+#include "qr_gemm_shapes.h"
 
 namespace qr {
 
@@ -468,42 +470,6 @@ gemm_rb_kernel(GemmParams p) {
 }
 
 
-// Shapes {TM, TN, NW}: BM = 32 TM, BN = 32 TN NW.
-//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K: QR_RB_BIG_K,
-//                  default 4, 1, 8 -> 128 x 256 with two waves per SIMD, whose
-//                  heavier decode then overlaps the other wave's MFMAs)
-//   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
-//                  of 128 x 256 at the same K split, half the reduction)
-//   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
-#ifndef QR_RB_BIG
-#define QR_RB_BIG 4, 2, 4
-#endif
-#ifndef QR_RB_BIG_K
-#define QR_RB_BIG_K 4, 1, 8
-#endif
-#ifndef QR_RB_MID
-#define QR_RB_MID 4, 1, 4
-#endif
-template <int TM, int TN, int NW> struct ShapeOf {
-    static constexpr uint32_t bm = 32 * TM, bn = 32 * TN * NW;
-};
-struct RbShape {
-    uint32_t bm, bn;
-};
-static int rb_pick(int format, uint32_t M, bool dual) {
-    if (dual) return 2;
-    if (M >= 1024) return format == QUANT_Q4_K ? 3 : 0;
-    return 1;
-}
-static RbShape rb_dims(int s) {
-    switch (s) {
-        case 0: return {ShapeOf<QR_RB_BIG>::bm, ShapeOf<QR_RB_BIG>::bn};
-        case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
-        case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
-        default: return {128, 128};
-    }
-}
-
 template <int F, int TM, int TN, int NW, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     using C = rb::Cfg<TM, TN, NW, DUAL>;
@@ -528,47 +494,14 @@ static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
     }
 }
 
-hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
-    GemmParams p = p0;
-    p.group_m = gemm_group_m(p);
-    const bool dual = p.W2 != nullptr;
-    switch (p.format) {
-        case QUANT_Q4_0: return dual ? rb_launch_fmt<QUANT_Q4_0, true>(p, st) : rb_launch_fmt<QUANT_Q4_0, false>(p, st);
-        case QUANT_MLX_4BIT: return dual ? rb_launch_fmt<QUANT_MLX_4BIT, true>(p, st) : rb_launch_fmt<QUANT_MLX_4BIT, false>(p, st);
-        case QUANT_Q4_K: return dual ? rb_launch_fmt<QUANT_Q4_K, true>(p, st) : rb_launch_fmt<QUANT_Q4_K, false>(p, st);
-        case QUANT_TERNARY_1_58: return dual ? rb_launch_fmt<QUANT_TERNARY_1_58, true>(p, st) : rb_launch_fmt<QUANT_TERNARY_1_58, false>(p, st);
-        case QUANT_VAR_RATE_AFFINE: return dual ? rb_launch_fmt<QUANT_VAR_RATE_AFFINE, true>(p, st) : rb_launch_fmt<QUANT_VAR_RATE_AFFINE, false>(p, st);
-        case QUANT_EXL3: return dual ? rb_launch_fmt<QUANT_EXL3, true>(p, st) : rb_launch_fmt<QUANT_EXL3, false>(p, st);
-        case QUANT_Q8_0: return dual ? rb_launch_fmt<QUANT_Q8_0, true>(p, st) : rb_launch_fmt<QUANT_Q8_0, false>(p, st);
-        case QUANT_PRISM_Q2_0: return dual ? rb_launch_fmt<QUANT_PRISM_Q2_0, true>(p, st) : rb_launch_fmt<QUANT_PRISM_Q2_0, false>(p, st);
-        default: return hipErrorInvalidValue;
-    }
+template <int F>
+hipError_t launch_gemm_format(const GemmParams& p, hipStream_t st) {
+    return p.W2 ? rb_launch_fmt<F, true>(p, st) : rb_launch_fmt<F, false>(p, st);
 }
 
-uint32_t gemm_pick_ksplit(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
-    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
-    // One workgroup fits a CU (its registers), so the grid runs in waves of
-    // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
-    // >= 512 of K per split) while the grid still fits one such wave.
-    uint32_t ks = 1;
-    while (T * ks * 2 <= 256 && p.K % (256 * ks * 2) == 0 && p.K / (ks * 2) >= 512) ks *= 2;
-    return ks;
-}
-
-size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
-    const bool dual = p.W2 != nullptr;
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, dual));
-    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
-    if (tiles) *tiles = T;
-    return ks > 1 ? (size_t)ks * T * d.bm * d.bn * (dual ? 2 : 1) : 0;
-}
-
-uint32_t gemm_group_m(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
-    const uint32_t nt_m = (p.M + d.bm - 1) / d.bm;
-    return nt_m >= 4 ? 4u : 2u;
-}
+#ifndef QR_GEMM_FORMAT
+#error "build qr_gemm.hip with -DQR_GEMM_FORMAT=<format id>"
+#endif
+template hipError_t launch_gemm_format<QR_GEMM_FORMAT>(const GemmParams& p, hipStream_t st);
 
 }  // namespace qr
-

@@ -1,0 +1,51 @@
+// qr_gemm_shapes.h -- tile shapes of the tiled projection kernel (qr_gemm.hip),
+// shared by the per-format kernel units and the host-side launch helpers.
+#pragma once
+#include "qr_formats.h"
+#include "qr_kernels.h"
+
+namespace qr {
+
+// Shapes {TM, TN, NW}: BM = 32 TM, BN = 32 TN NW.
+//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K: QR_RB_BIG_K,
+//                  default 4, 1, 8 -> 128 x 256 with two waves per SIMD, whose
+//                  heavier decode then overlaps the other wave's MFMAs)
+//   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
+//                  of 128 x 256 at the same K split, half the reduction)
+//   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
+#ifndef QR_RB_BIG
+#define QR_RB_BIG 4, 2, 4
+#endif
+#ifndef QR_RB_BIG_K
+#define QR_RB_BIG_K 4, 1, 8
+#endif
+#ifndef QR_RB_MID
+#define QR_RB_MID 4, 1, 4
+#endif
+template <int TM, int TN, int NW> struct ShapeOf {
+    static constexpr uint32_t bm = 32 * TM, bn = 32 * TN * NW;
+};
+struct RbShape {
+    uint32_t bm, bn;
+};
+inline int rb_pick(int format, uint32_t M, bool dual) {
+    if (dual) return 2;
+    if (M >= 1024) return format == QUANT_Q4_K ? 3 : 0;
+    return 1;
+}
+inline RbShape rb_dims(int s) {
+    switch (s) {
+        case 0: return {ShapeOf<QR_RB_BIG>::bm, ShapeOf<QR_RB_BIG>::bn};
+        case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
+        case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
+        default: return {128, 128};
+    }
+}
+
+// Launches the tiled kernel of format F (plain, or the SwiGLU dual variant when
+// p.W2 is set); one explicit instantiation per format, each in its own
+// compilation unit (qr_gemm.hip built with -DQR_GEMM_FORMAT=F).
+template <int F>
+hipError_t launch_gemm_format(const GemmParams& p, hipStream_t st);
+
+}  // namespace qr
