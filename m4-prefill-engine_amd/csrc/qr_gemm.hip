@@ -49,9 +49,6 @@ namespace qr {
 #ifndef QR_RB_VPM
 #define QR_RB_VPM 5
 #endif
-#ifndef QR_RB_ADIST
-#define QR_RB_ADIST 1
-#endif
 
 
 namespace rb {
@@ -203,11 +200,7 @@ gemm_rb_kernel(GemmParams p) {
     };
 
     uint32_t bw[2][NCB][16];
-    // A fragments are read AD slices ahead of the MFMAs that use them (ring of
-    // AD + 1 slots; slice t = 4 j + kk of the unrolled group uses slot t % (AD + 1)).
-    constexpr int AD = QR_RB_ADIST;
-    static_assert((4 * U) % (AD + 1) == 0, "A ring divides the unrolled slices");
-    h8_t af[AD + 1][TM];
+    h8_t af[2][TM];
 
     // One K step, as four k-slices.  Slice kk: read the A fragments of slice
     // kk + 1 (of step s + 1 for the last slice), the TM x NCB MFMAs of slice kk,
@@ -225,16 +218,15 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             __builtin_amdgcn_sched_barrier(0);
-            const int t = 4 * j + kk;
-            if (kk + AD < 4) read_a(j % XS, kk + AD, af[(t + AD) % (AD + 1)]);
-            else read_a((j + 1) % XS, kk + AD - 4, af[(t + AD) % (AD + 1)]);
+            if (kk < 3) read_a(j % XS, kk + 1, af[(kk + 1) & 1]);
+            else read_a((j + 1) % XS, 0, af[0]);
 #pragma unroll
             for (int jb = 0; jb < NCB; jb++) {
                 const uint32_t* bj = bw[j & 1][jb];
                 const h8_t b = __builtin_bit_cast(h8_t, u4_t{bj[4 * kk], bj[4 * kk + 1], bj[4 * kk + 2], bj[4 * kk + 3]});
 #pragma unroll
                 for (int i = 0; i < TM; i++)
-                    acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t % (AD + 1)][i], b, acc[i][jb], 0, 0, 0);
+                    acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], b, acc[i][jb], 0, 0, 0);
             }
             if (kk < HALVES) {
                 const int jb = kk >> 1, hh = kk & 1;
@@ -251,7 +243,9 @@ gemm_rb_kernel(GemmParams p) {
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (F == QUANT_Q4_K) {
+        if constexpr (F == QUANT_Q4_K || F == QUANT_Q4_0) {
+            // wave-uniform slow path: re-decode exactly when any lane's group
+            // needs it (Q4_K binade gap; Q4_0 scales with -8 d not finite)
             bool slow = false;
 #pragma unroll
             for (int jb = 0; jb < NCB; jb++)
@@ -278,8 +272,7 @@ gemm_rb_kernel(GemmParams p) {
     decode(0, 0, bw[0]);
     load_w(WP, 0);
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < AD; t++) read_a(0, t, af[t]);
+    read_a(0, 0, af[0]);
 
     // ---- main loop: full groups of U steps branch-free (look-ahead fetches past
     // the K range read zeros), then the remainder with guards ----

@@ -133,6 +133,27 @@ def test_gemm_var_rate_and_exl3(bridge, oracle, fmt, M, K, N):
     tolerance.check(host(Yh), refh, tolerance.gemm_bound(refh, axw.reshape(M, H, D).transpose(1, 0, 2), K))
 
 
+def test_gemm_q4_0_scales_beyond_fast_path(bridge, oracle):
+    """Q4_0 scales with |d| > 8188 (-8 d is not finite in binary16): the tiled
+    kernel's fused fma(q, d, -8 d) decode cannot form them, so the wave takes
+    the exact (q - 8) d path; codes 1..15 keep every weight finite."""
+    M, K, N = 129, 512, 128
+    rng = np.random.default_rng(77)
+    W = synth.random_blocks(0, N, K, 78).reshape(N, K // 32, 18).copy()
+    d = (rng.random((N, K // 32)) * 800 + 8190) * np.where(rng.random((N, K // 32)) < 0.5, -1, 1)
+    W[..., 0:2] = d.astype(np.float16)[..., None].view(np.uint8)
+    lo = rng.integers(1, 16, (N, K // 32, 16))
+    hi = rng.integers(1, 16, (N, K // 32, 16))
+    W[..., 2:] = (lo | (hi << 4)).astype(np.uint8)
+    W = W.reshape(-1)
+    X = synth.activations(M, K, 79, std=1e-5)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, 0, M, K, N)
+    bridge.synchronize()
+    ref = oracle.gemm(0, X, W, N)
+    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, 0, X, W, K, N), K))
+
+
 @pytest.mark.parametrize("fmt", [6, 7])
 @pytest.mark.parametrize("M,K,N", [(1, 384, 256), (33, 384, 200), (129, 512, 256), (128, 4096, 320),
                                    (300, 1152, 136)])
