@@ -29,6 +29,17 @@ def test_exports_every_declared_symbol(lib):
     assert names == set(m4_bridge.SIGNATURES), "bindings and header disagree"
 
 
+def test_exports_every_gguf_symbol(lib):
+    import gguf
+
+    header = (ROOT / "include" / "m4_gguf.h").read_text()
+    names = set(re.findall(r"^M4_API [\w\s\*]*?\b(m4_\w+)\s*\(", header, re.M))
+    assert len(names) >= 20
+    for n in sorted(names):
+        assert hasattr(lib, n), f"missing export {n}"
+    assert names == set(gguf.SIGNATURES), "bindings and header disagree"
+
+
 def test_expected_weight_bytes(lib):
     # core/bridge/m4_mlx_bridge.mm:58-75
     K, N = 4096, 4096

@@ -481,3 +481,26 @@ def test_tiled_split_k(bridge, oracle, fmt, M):
     bridge.synchronize()
     assert maxdiff(host(Y), oracle.gemm(fmt, X, W, N)) <= TOL
     assert maxdiff(host(Yr), oracle.gemm(fmt, X, W, N, R=R)) <= TOL
+
+
+def test_gguf_q4_k_tensor_feeds_the_projection(bridge, oracle):
+    """A GGML-standard Q4_K tensor read from a GGUF buffer and repacked by
+    m4_gguf_load_router_weights drives the tiled projection kernel."""
+    import gguf
+    from test_gguf import ggml_pack_q4_k, make_gguf
+
+    rng = np.random.default_rng(31)
+    M, K, N = 129, 1024, 192
+    nb = N * K // 256
+    q4k = ggml_pack_q4_k((rng.random(nb) * 0.004 + 1e-4).astype(np.float16), (rng.random(nb) * 0.004).astype(np.float16),
+                         rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8)), rng.integers(0, 16, (nb, 256)))
+    ld = gguf.GGUFLoader()
+    assert ld.parse_from_buffer(make_gguf([], [("blk.0.ffn_up.weight", [K, N], gguf.GGML_Q4_K, q4k.tobytes())]))
+    W, fmt, k, n = ld.load_router_weights("blk.0.ffn_up.weight")
+    assert (fmt, k, n) == (2, K, N)
+    X = synth.activations(M, K, 32)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    ref = oracle.gemm(2, X, W, N)
+    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, 2, X, W, K, N), K))
