@@ -136,6 +136,44 @@ M4_API int m4_bridge_prefill_layer(void* X_ptr, void* Wq, void* Wk, void* Wv, vo
                             void* Wd, void* X_out, int format, uint32_t M, uint32_t d_model, uint32_t H,
                             uint32_t D, uint32_t N_mlp, float attn_scale);
 
+/* Grouped-query variant: K/V carry Hkv heads ([Hkv, M, D] Q8_0 blocks) and
+ * query head h reads KV head h / (H / Hkv) (H % Hkv == 0), as the MLX block
+ * passes them to scaled_dot_product_attention (src/engine/model.py:234-236).
+ * Hkv == H is m4_bridge_dispatch_flash_attn_q8_0. */
+M4_API int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q_ptr, size_t Q_bytes, void* Kq_ptr, size_t Kq_bytes,
+                                           void* Vq_ptr, size_t Vq_bytes, void* O_ptr, size_t O_bytes,
+                                           uint32_t H, uint32_t Hkv, uint32_t M, uint32_t D, float scale,
+                                           int o_token_major);
+
+/* RMSNorm of the MLX block (src/engine/model.py:17-48) over rows of X [M, D]
+ * (D % 8 == 0): Y = fp16(fp16(x / sqrt(mean(x^2) + eps)) * w) for norm_type 1
+ * ("rmsnorm"), with fp16(1 + w) in place of w for norm_type 2
+ * ("gemma_add_one").  W fp16 [D].  Codes: -1, -2 (null / short buffers),
+ * -3 (norm_type), -4 (dims), -5, -6 as dispatch_gemm. */
+M4_API int m4_bridge_rmsnorm(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes, void* Y_ptr,
+                      size_t Y_bytes, uint32_t M, uint32_t D, float eps, int norm_type);
+
+/* Rotary position embedding in place on T [H, M, D] (D % 16 == 0): nn.RoPE
+ * (dims = D, traditional, base = theta) applied at positions offset + m
+ * (src/engine/model.py:112-116, :215-226).  Pairs (i, i + D/2), or (2i, 2i + 1)
+ * when traditional, rotate by (offset + m) theta^(-2i/D). */
+M4_API int m4_bridge_rope(void* T_ptr, size_t T_bytes, uint32_t H, uint32_t M, uint32_t D, float theta,
+                   uint32_t offset, int traditional);
+
+/* The MLX transformer block (src/engine/model.py:181-265) on the router's
+ * kernels: RMSNorm(X, w_attn) -> Q [Hq], K, V [Hkv] head GEMMs -> RoPE(Q, K)
+ * -> Q8_0(K, V) -> grouped-query flash attention -> O-proj + residual ->
+ * RMSNorm(w_ffn) -> fused SwiGLU -> down-proj + residual.  w_attn / w_ffn
+ * fp16 [d_model] or NULL (no norm); rope = 0 skips RoPE.  Wq [Hq*D, d_model],
+ * Wk/Wv [Hkv*D, d_model], Wo [d_model, Hq*D], Wg/Wu [N_mlp, d_model],
+ * Wd [d_model, N_mlp].  Device pointers, 16-byte aligned; X_out must not
+ * alias X.  Hkv == Hq, no norms, no RoPE is m4_bridge_prefill_layer. */
+M4_API int m4_bridge_prefill_layer_ex(void* X_ptr, void* w_attn, void* Wq, void* Wk, void* Wv, void* Wo,
+                               void* w_ffn, void* Wg, void* Wu, void* Wd, void* X_out, int format,
+                               uint32_t M, uint32_t d_model, uint32_t Hq, uint32_t Hkv, uint32_t D,
+                               uint32_t N_mlp, float attn_scale, int norm_type, float norm_eps, int rope,
+                               float rope_theta, uint32_t rope_offset, int rope_traditional);
+
 /* Dequantize W [N, K] to fp16 [N, K] with the kernels' own decoders (the
  * registry's dequantize hook, src/router/quant_registry.h:24). Formats 0..7. */
 M4_API int m4_bridge_dequantize(void* W_ptr, size_t W_bytes, void* out_ptr, size_t out_bytes, int format,

@@ -243,8 +243,9 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
     const size_t head_elems = (size_t)M * D;
     const _Float16* Qh = p.Q + (size_t)h * head_elems;
     const uint32_t kv_bytes = (uint32_t)(head_elems / 32 * 34);
-    auto kr = make_rsrc(p.Kq + (size_t)h * (head_elems / 32) * 34, kv_bytes);
-    auto vr = make_rsrc(p.Vq + (size_t)h * (head_elems / 32) * 34, kv_bytes);
+    const int hk = p.Hkv ? h / ((int)p.H / (int)p.Hkv) : h;  // grouped-query: shared KV head
+    auto kr = make_rsrc(p.Kq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
+    auto vr = make_rsrc(p.Vq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
 
     const int q_last = min(q0 + kBQ, M) - 1;
     const int ntiles = q_last / kBKV + 1;

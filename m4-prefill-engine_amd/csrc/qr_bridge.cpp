@@ -350,24 +350,24 @@ int m4_bridge_quantize_kv_q8_0(void* src, size_t src_bytes, void* dst, size_t ds
     return 0;
 }
 
-int m4_bridge_dispatch_flash_attn_q8_0(void* Q, size_t Qb, void* Kq, size_t Kqb, void* Vq, size_t Vqb, void* O,
-                                       size_t Ob, uint32_t H, uint32_t M, uint32_t D, float scale,
-                                       int o_token_major) {
+int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t Kqb, void* Vq, size_t Vqb, void* O,
+                                           size_t Ob, uint32_t H, uint32_t Hkv, uint32_t M, uint32_t D, float scale,
+                                           int o_token_major) {
     if (!g_initialized) return -1;
     if (!Q || !Kq || !Vq || !O) return -2;
     if ((reinterpret_cast<uintptr_t>(Q) % 2) || (reinterpret_cast<uintptr_t>(O) % 2)) return -2;
-    if (H == 0 || M == 0 || (D != 64 && D != 128)) return -4;
-    const size_t n = (size_t)H * M * D;
-    if (Qb < n * 2 || Ob < n * 2 || Kqb < n / 32 * 34 || Vqb < n / 32 * 34) return -2;
+    if (H == 0 || M == 0 || Hkv == 0 || H % Hkv || (D != 64 && D != 128)) return -4;
+    const size_t n = (size_t)H * M * D, nk = (size_t)Hkv * M * D;
+    if (Qb < n * 2 || Ob < n * 2 || Kqb < nk / 32 * 34 || Vqb < nk / 32 * 34) return -2;
     std::lock_guard<std::mutex> lk(g_mu);
     void* dq = resolve(Q, n * 2, 16, true, false);
-    void* dk = resolve(Kq, n / 32 * 34, 4, true, false);
-    void* dv = resolve(Vq, n / 32 * 34, 4, true, false);
+    void* dk = resolve(Kq, nk / 32 * 34, 4, true, false);
+    void* dv = resolve(Vq, nk / 32 * 34, 4, true, false);
     void* dout = resolve(O, n * 2, 8, false, true);
     if (!dq || !dk || !dv || !dout) return -5;
     qr::AttnParams p{static_cast<const _Float16*>(dq), static_cast<const uint8_t*>(dk),
                      static_cast<const uint8_t*>(dv), static_cast<_Float16*>(dout), H, M, D, scale,
-                     o_token_major ? 1 : 0};
+                     o_token_major ? 1 : 0, Hkv};
     hipError_t e = qr::launch_flash_attn_q8_0(p, g_stream);
     finish_outputs();
     if (e != hipSuccess) {
@@ -375,6 +375,12 @@ int m4_bridge_dispatch_flash_attn_q8_0(void* Q, size_t Qb, void* Kq, size_t Kqb,
         return -6;
     }
     return 0;
+}
+
+int m4_bridge_dispatch_flash_attn_q8_0(void* Q, size_t Qb, void* Kq, size_t Kqb, void* Vq, size_t Vqb, void* O,
+                                       size_t Ob, uint32_t H, uint32_t M, uint32_t D, float scale,
+                                       int o_token_major) {
+    return m4_bridge_dispatch_flash_attn_q8_0_gqa(Q, Qb, Kq, Kqb, Vq, Vqb, O, Ob, H, H, M, D, scale, o_token_major);
 }
 
 int m4_bridge_dequantize(void* W, size_t Wb, void* out, size_t outb, int format, uint32_t K, uint32_t N) {
@@ -405,23 +411,41 @@ int m4_bridge_prefill_layer(void* X, void* Wq, void* Wk, void* Wv, void* Wo, voi
                             void* Xout, int format, uint32_t M, uint32_t dm, uint32_t H, uint32_t D, uint32_t Nm,
                             float scale) {
     if (!g_initialized) return -1;
+    if (!Wq || !Wk || !Wv || !Wo || !Wg || !Wu || !Wd) return -2;
+    return m4_bridge_prefill_layer_ex(X, nullptr, Wq, Wk, Wv, Wo, nullptr, Wg, Wu, Wd, Xout, format, M, dm, H, H, D,
+                                      Nm, scale, 1, 0.0f, 0, 10000.0f, 0, 0);
+}
+
+int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* Wv, void* Wo, void* w_ffn, void* Wg,
+                               void* Wu, void* Wd, void* Xout, int format, uint32_t M, uint32_t dm, uint32_t Hq,
+                               uint32_t Hkv, uint32_t D, uint32_t Nm, float scale, int norm_type, float eps,
+                               int rope, float theta, uint32_t offset, int traditional) {
+    if (!g_initialized) return -1;
     void* ptrs[9] = {X, Wq, Wk, Wv, Wo, Wg, Wu, Wd, Xout};
     for (void* q : ptrs)
         if (!q) return -2;
     if (!has_kernels(format)) return -3;
-    if (M == 0 || dm == 0 || H == 0 || Nm == 0 || (D != 64 && D != 128)) return -4;
-    const uint32_t HD = H * D;
+    if ((w_attn || w_ffn) && norm_type != 1 && norm_type != 2) return -3;
+    if (M == 0 || dm == 0 || Hq == 0 || Hkv == 0 || Hq % Hkv || Nm == 0 || (D != 64 && D != 128)) return -4;
+    const uint32_t HQ = Hq * D, HK = Hkv * D;
     const uint32_t bs = qr::get_quant_info(static_cast<qr::QuantFormat>(format)).block_size;
-    if (dm % bs || HD % bs || Nm % bs || dm % 32 || HD % 32 || Nm % 32) return -4;
+    if (dm % bs || HQ % bs || Nm % bs || dm % 32 || HQ % 32 || Nm % 32) return -4;
     for (void* q : ptrs) {
         void* d = device_view(q);
         if (!d || d != q || (reinterpret_cast<uintptr_t>(q) % 16)) return -2;  // device, 16-byte aligned
     }
+    for (void* q : {w_attn, w_ffn}) {
+        if (!q) continue;
+        void* d = device_view(q);
+        if (!d || d != q || (reinterpret_cast<uintptr_t>(q) % 16)) return -2;
+    }
     std::lock_guard<std::mutex> lk(g_mu);
-    const size_t nqkv = (size_t)M * HD;
-    const size_t q8 = nqkv / 32 * 34;
+    const size_t nq = (size_t)M * HQ, nk = (size_t)M * HK;
+    const size_t q8 = nk / 32 * 34;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    const size_t need = 3 * al(nqkv * 2) + 2 * al(q8) + al(nqkv * 2) + al((size_t)M * dm * 2) + al((size_t)M * Nm * 2);
+    const bool norms = w_attn || w_ffn;
+    const size_t need = 2 * al(nq * 2) + 2 * al(nk * 2) + 2 * al(q8) + al((size_t)M * dm * 2) +
+                        al((size_t)M * Nm * 2) + (norms ? al((size_t)M * dm * 2) : 0);
     if (need > g_ws_bytes) {
         if (g_ws) {
             (void)hipStreamSynchronize(g_stream);
@@ -438,14 +462,15 @@ int m4_bridge_prefill_layer(void* X, void* Wq, void* Wk, void* Wv, void* Wo, voi
     }
     uint8_t* w = static_cast<uint8_t*>(g_ws);
     auto take = [&](size_t b) { uint8_t* r = w; w += al(b); return r; };
-    _Float16* q = reinterpret_cast<_Float16*>(take(nqkv * 2));
-    _Float16* k = reinterpret_cast<_Float16*>(take(nqkv * 2));
-    _Float16* v = reinterpret_cast<_Float16*>(take(nqkv * 2));
+    _Float16* q = reinterpret_cast<_Float16*>(take(nq * 2));
+    _Float16* k = reinterpret_cast<_Float16*>(take(nk * 2));
+    _Float16* v = reinterpret_cast<_Float16*>(take(nk * 2));
     uint8_t* kq = take(q8);
     uint8_t* vq = take(q8);
-    _Float16* o = reinterpret_cast<_Float16*>(take(nqkv * 2));
+    _Float16* o = reinterpret_cast<_Float16*>(take(nq * 2));
     _Float16* xm = reinterpret_cast<_Float16*>(take((size_t)M * dm * 2));
     _Float16* s = reinterpret_cast<_Float16*>(take((size_t)M * Nm * 2));
+    _Float16* xn = norms ? reinterpret_cast<_Float16*>(take((size_t)M * dm * 2)) : nullptr;
 
     auto proj = [&](const void* A, const void* W, const void* W2, _Float16* Y, const _Float16* R, uint32_t N,
                     uint32_t Kd, uint32_t headD) {
@@ -461,24 +486,83 @@ int m4_bridge_prefill_layer(void* X, void* Wq, void* Wk, void* Wv, void* Wo, voi
         p.col_bytes = qr::kernel_weight_bytes(format, Kd, N) / N;
         return launch(p);
     };
+    auto check = [&](hipError_t e, const char* what) {
+        if (e == hipSuccess) return 0;
+        set_error(what, e);
+        return -6;
+    };
     int rc = 0;
-    rc = rc ? rc : proj(X, Wq, nullptr, q, nullptr, HD, dm, D);
-    rc = rc ? rc : proj(X, Wk, nullptr, k, nullptr, HD, dm, D);
-    rc = rc ? rc : proj(X, Wv, nullptr, v, nullptr, HD, dm, D);
-    if (!rc) {
-        hipError_t e = qr::launch_quantize_q8_0(k, kq, nqkv / 32, g_stream);
-        if (e == hipSuccess) e = qr::launch_quantize_q8_0(v, vq, nqkv / 32, g_stream);
-        qr::AttnParams ap{q, kq, vq, o, H, M, D, scale, 1};
-        if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(ap, g_stream);
-        if (e != hipSuccess) {
-            set_error("layer attention", e);
-            rc = -6;
-        }
+    const void* a = X;
+    if (w_attn) {
+        rc = check(qr::launch_rmsnorm(static_cast<const _Float16*>(X), static_cast<const _Float16*>(w_attn), xn, M, dm,
+                                      eps, norm_type, g_stream), "layer rmsnorm");
+        a = xn;
     }
-    rc = rc ? rc : proj(o, Wo, nullptr, xm, static_cast<const _Float16*>(X), dm, HD, 0);
-    rc = rc ? rc : proj(xm, Wg, Wu, s, nullptr, Nm, dm, 0);
+    rc = rc ? rc : proj(a, Wq, nullptr, q, nullptr, HQ, dm, D);
+    rc = rc ? rc : proj(a, Wk, nullptr, k, nullptr, HK, dm, D);
+    rc = rc ? rc : proj(a, Wv, nullptr, v, nullptr, HK, dm, D);
+    if (!rc && rope) {
+        rc = check(qr::launch_rope(q, Hq, M, D, theta, offset, traditional, g_stream), "layer rope");
+        rc = rc ? rc : check(qr::launch_rope(k, Hkv, M, D, theta, offset, traditional, g_stream), "layer rope");
+    }
+    if (!rc) {
+        hipError_t e = qr::launch_quantize_q8_0(k, kq, nk / 32, g_stream);
+        if (e == hipSuccess) e = qr::launch_quantize_q8_0(v, vq, nk / 32, g_stream);
+        qr::AttnParams ap{q, kq, vq, o, Hq, M, D, scale, 1, Hkv};
+        if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(ap, g_stream);
+        rc = check(e, "layer attention");
+    }
+    rc = rc ? rc : proj(o, Wo, nullptr, xm, static_cast<const _Float16*>(X), dm, HQ, 0);
+    a = xm;
+    if (!rc && w_ffn) {
+        rc = check(qr::launch_rmsnorm(xm, static_cast<const _Float16*>(w_ffn), xn, M, dm, eps, norm_type, g_stream),
+                   "layer rmsnorm");
+        a = xn;
+    }
+    rc = rc ? rc : proj(a, Wg, Wu, s, nullptr, Nm, dm, 0);
     rc = rc ? rc : proj(s, Wd, nullptr, static_cast<_Float16*>(Xout), xm, dm, Nm, 0);
     return rc;
+}
+
+int m4_bridge_rmsnorm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, uint32_t M, uint32_t D, float eps,
+                      int norm_type) {
+    if (!g_initialized) return -1;
+    if (!X || !W || !Y) return -2;
+    if (norm_type != 1 && norm_type != 2) return -3;
+    if (M == 0 || D == 0 || D % 8) return -4;
+    if (Xb < (size_t)M * D * 2 || Yb < (size_t)M * D * 2 || Wb < (size_t)D * 2) return -2;
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* dx = resolve(X, (size_t)M * D * 2, 16, true, false);
+    void* dw = resolve(W, (size_t)D * 2, 16, true, false);
+    void* dy = resolve(Y, (size_t)M * D * 2, 16, false, true);
+    if (!dx || !dw || !dy) return -5;
+    hipError_t e = qr::launch_rmsnorm(static_cast<const _Float16*>(dx), static_cast<const _Float16*>(dw),
+                                      static_cast<_Float16*>(dy), M, D, eps, norm_type, g_stream);
+    finish_outputs();
+    if (e != hipSuccess) {
+        set_error("rmsnorm", e);
+        return -6;
+    }
+    return 0;
+}
+
+int m4_bridge_rope(void* T, size_t Tb, uint32_t H, uint32_t M, uint32_t D, float theta, uint32_t offset,
+                   int traditional) {
+    if (!g_initialized) return -1;
+    if (!T) return -2;
+    if (H == 0 || M == 0 || D == 0 || D % 16 || !(theta > 0.0f)) return -4;
+    const size_t n = (size_t)H * M * D * 2;
+    if (Tb < n) return -2;
+    std::lock_guard<std::mutex> lk(g_mu);
+    void* dt = resolve(T, n, 16, true, true);
+    if (!dt) return -5;
+    hipError_t e = qr::launch_rope(static_cast<_Float16*>(dt), H, M, D, theta, offset, traditional, g_stream);
+    finish_outputs();
+    if (e != hipSuccess) {
+        set_error("rope", e);
+        return -6;
+    }
+    return 0;
 }
 
 void m4_bridge_synchronize(void) {

@@ -45,13 +45,24 @@ hipError_t launch_quantize_q8_0(const _Float16* src, uint8_t* dst, size_t num_bl
 
 struct AttnParams {
     const _Float16* Q;    // [H, M, D]
-    const uint8_t* Kq;    // Q8_0 blocks over [H, M, D]
-    const uint8_t* Vq;    // Q8_0 blocks over [H, M, D]
+    const uint8_t* Kq;    // Q8_0 blocks over [Hkv, M, D]
+    const uint8_t* Vq;    // Q8_0 blocks over [Hkv, M, D]
     _Float16* O;          // [H, M, D] or token-major [M, H * D]
     uint32_t H, M, D;
     float scale;
     int o_token_major;
+    uint32_t Hkv;         // KV heads (grouped-query: query head h reads KV head h / (H / Hkv)); 0 = H
 };
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st);
+
+// RMSNorm over rows of X [M, D] (D % 8 == 0): y = fp16(fp16(x r) w), r =
+// 1 / sqrt(mean(x^2) + eps); norm_type 2 uses fp16(1 + w) in place of w.
+hipError_t launch_rmsnorm(const _Float16* X, const _Float16* w, _Float16* Y, uint32_t M, uint32_t D, float eps,
+                          int norm_type, hipStream_t st);
+// Rotary position embedding in place on T [H, M, D] (D % 16 == 0), positions
+// offset + m, frequencies theta^(-2i/D); pairs (i, i + D/2), or (2i, 2i + 1)
+// when traditional.
+hipError_t launch_rope(_Float16* T, uint32_t H, uint32_t M, uint32_t D, float theta, uint32_t offset,
+                       int traditional, hipStream_t st);
 
 }  // namespace qr

@@ -69,6 +69,12 @@ SIGNATURES = {
     "m4_bridge_quantize_kv_q8_0": ([_VP, _SZ, _VP, _SZ, ctypes.c_uint64], _I),
     "m4_bridge_dispatch_flash_attn_q8_0": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, _U32, _U32, _U32, _F, _I], _I),
     "m4_bridge_prefill_layer": ([_VP] * 9 + [_I, _U32, _U32, _U32, _U32, _U32, _F], _I),
+    "m4_bridge_dispatch_flash_attn_q8_0_gqa": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, _U32, _U32, _U32, _U32, _F,
+                                                _I], _I),
+    "m4_bridge_rmsnorm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _U32, _U32, _F, _I], _I),
+    "m4_bridge_rope": ([_VP, _SZ, _U32, _U32, _U32, _F, _U32, _I], _I),
+    "m4_bridge_prefill_layer_ex": ([_VP] * 11 + [_I, _U32, _U32, _U32, _U32, _U32, _U32, _F, _I, _F, _I, _F, _U32,
+                                                 _I], _I),
     "m4_bridge_dequantize": ([_VP, _SZ, _VP, _SZ, _I, _U32, _U32], _I),
     "m4_bridge_set_stream": ([_VP], _I),
     "m4_bridge_get_stream": ([], _VP),
@@ -326,6 +332,52 @@ class HIPBridge:
         self._bind_stream(*bufs)
         ret = self._lib.m4_bridge_prefill_layer(*ptrs, int(format), M, d_model, H, D, N_mlp, float(attn_scale))
         self._check("m4_bridge_prefill_layer", ret)
+        self._in_flight_tensors.append(bufs)
+        return ret
+
+    def dispatch_flash_attn_q8_0_gqa(self, Q, Kq, Vq, O, H, Hkv, M, D, scale, o_token_major: bool = False) -> int:
+        """Grouped-query causal attention: K/V hold Hkv heads (src/engine/model.py:234-236)."""
+        a = [self.extract_buffer_address_and_size(t) for t in (Q, Kq, Vq, O)]
+        self._bind_stream(Q, Kq, Vq, O)
+        ret = self._lib.m4_bridge_dispatch_flash_attn_q8_0_gqa(a[0][0], a[0][1], a[1][0], a[1][1], a[2][0], a[2][1],
+                                                               a[3][0], a[3][1], H, Hkv, M, D, float(scale),
+                                                               int(bool(o_token_major)))
+        self._check("m4_bridge_dispatch_flash_attn_q8_0_gqa", ret)
+        self._in_flight_tensors.append((Q, Kq, Vq, O))
+        return ret
+
+    def rmsnorm(self, X, w, Y, eps: float = 1e-5, norm_type: int = 1) -> int:
+        """RMSNorm over the rows of X [M, D] (src/engine/model.py:39-48); norm_type 2 = gemma_add_one."""
+        a = [self.extract_buffer_address_and_size(t) for t in (X, w, Y)]
+        M, D = X.shape
+        self._bind_stream(X, w, Y)
+        ret = self._lib.m4_bridge_rmsnorm(a[0][0], a[0][1], a[1][0], a[1][1], a[2][0], a[2][1], M, D, float(eps),
+                                          int(norm_type))
+        self._check("m4_bridge_rmsnorm", ret)
+        self._in_flight_tensors.append((X, w, Y))
+        return ret
+
+    def rope(self, T, theta: float = 10000.0, offset: int = 0, traditional: bool = False) -> int:
+        """RoPE in place on T [H, M, D] (nn.RoPE, src/engine/model.py:112-116)."""
+        ptr, nbytes = self.extract_buffer_address_and_size(T)
+        H, M, D = T.shape
+        self._bind_stream(T)
+        ret = self._lib.m4_bridge_rope(ptr, nbytes, H, M, D, float(theta), int(offset), int(bool(traditional)))
+        self._check("m4_bridge_rope", ret)
+        self._in_flight_tensors.append((T,))
+        return ret
+
+    def prefill_layer_ex(self, X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, X_out, format, M, d_model, Hq, Hkv, D,
+                         N_mlp, attn_scale, norm_type: int = 1, norm_eps: float = 1e-5, rope: bool = True,
+                         rope_theta: float = 10000.0, rope_offset: int = 0, rope_traditional: bool = False) -> int:
+        """The MLX transformer block on the router's kernels (src/engine/model.py:181-265)."""
+        bufs = (X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, X_out)
+        ptrs = [None if t is None else self.extract_buffer_address_and_size(t)[0] for t in bufs]
+        self._bind_stream(*[t for t in bufs if t is not None])
+        ret = self._lib.m4_bridge_prefill_layer_ex(*ptrs, int(format), M, d_model, Hq, Hkv, D, N_mlp,
+                                                   float(attn_scale), int(norm_type), float(norm_eps), int(bool(rope)),
+                                                   float(rope_theta), int(rope_offset), int(bool(rope_traditional)))
+        self._check("m4_bridge_prefill_layer_ex", ret)
         self._in_flight_tensors.append(bufs)
         return ret
 

@@ -488,18 +488,19 @@ EXPORT void orc_dequantize_q8_0(const uint8_t* src, uint16_t* dst, size_t num_bl
 
 typedef struct {
     const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
-    uint32_t H, M, D; double scale; int o_token_major;
+    uint32_t H, M, D; double scale; int o_token_major; uint32_t Hkv;
 } attn_ctx;
 
 static void attn_head_row(void* vctx, size_t idx) {
     attn_ctx* c = (attn_ctx*)vctx;
     size_t h = idx / c->M, i = idx % c->M;
     size_t MD = (size_t)c->M * c->D;
+    size_t hk = h / (c->H / c->Hkv);  /* grouped-query: H / Hkv query heads per KV head */
     const uint16_t* q = c->Q + h * MD + i * c->D;
     double* s = (double*)malloc(sizeof(double) * (i + 1));
     double mx = -1e30;
     for (size_t j = 0; j <= i; j++) {
-        const uint16_t* k = c->K + h * MD + j * c->D;
+        const uint16_t* k = c->K + hk * MD + j * c->D;
         double dot = 0.0;
         for (uint32_t d = 0; d < c->D; d++) dot += orc_f16_to_f64(q[d]) * orc_f16_to_f64(k[d]);
         s[j] = dot * c->scale;
@@ -510,7 +511,7 @@ static void attn_head_row(void* vctx, size_t idx) {
     double inv = (sum > 0.0) ? 1.0 / sum : 0.0;
     for (uint32_t d = 0; d < c->D; d++) {
         double acc = 0.0;
-        for (size_t j = 0; j <= i; j++) acc += (s[j] * inv) * orc_f16_to_f64(c->V[h * MD + j * c->D + d]);
+        for (size_t j = 0; j <= i; j++) acc += (s[j] * inv) * orc_f16_to_f64(c->V[hk * MD + j * c->D + d]);
         size_t o = c->o_token_major ? (i * (size_t)c->H + h) * c->D + d : h * MD + i * c->D + d;
         c->O[o] = orc_f64_to_f16(acc);
     }
@@ -524,8 +525,20 @@ static void attn_head_row(void* vctx, size_t idx) {
 EXPORT void orc_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O,
                           uint32_t H, uint32_t M, uint32_t D, float scale, int o_token_major,
                           int nthreads) {
-    attn_ctx c = {Q, K, V, O, H, M, D, (double)scale, o_token_major};
+    attn_ctx c = {Q, K, V, O, H, M, D, (double)scale, o_token_major, H};
     parallel_rows(attn_head_row, &c, (size_t)H * M, nthreads);
+}
+
+/* Grouped-query attention (src/engine/model.py:234-236 passes Hkv < H heads of
+ * K/V to mx.fast.scaled_dot_product_attention): query head h reads KV head
+ * h / (H / Hkv).  K, V [Hkv, M, D]. */
+EXPORT int orc_attention_gqa(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O,
+                             uint32_t H, uint32_t Hkv, uint32_t M, uint32_t D, float scale,
+                             int o_token_major, int nthreads) {
+    if (!Hkv || H % Hkv) return -4;
+    attn_ctx c = {Q, K, V, O, H, M, D, (double)scale, o_token_major, Hkv};
+    parallel_rows(attn_head_row, &c, (size_t)H * M, nthreads);
+    return 0;
 }
 
 /* Attention over a Q8_0 KV cache: the reference checks its Q8_0 kernel
@@ -542,6 +555,77 @@ EXPORT void orc_attention_q8_0(const uint16_t* Q, const uint8_t* Kq, const uint8
     orc_attention(Q, Kd, Vd, O, H, M, D, scale, o_token_major, nthreads);
     free(Kd);
     free(Vd);
+}
+
+/* Same with Hkv KV heads (Kq/Vq blocks over [Hkv, M, D]). */
+EXPORT int orc_attention_q8_0_gqa(const uint16_t* Q, const uint8_t* Kq, const uint8_t* Vq, uint16_t* O,
+                                  uint32_t H, uint32_t Hkv, uint32_t M, uint32_t D, float scale,
+                                  int o_token_major, int nthreads) {
+    size_t n = (size_t)Hkv * M * D;
+    uint16_t* Kd = (uint16_t*)malloc(n * 2);
+    uint16_t* Vd = (uint16_t*)malloc(n * 2);
+    orc_dequantize_q8_0(Kq, Kd, n / 32);
+    orc_dequantize_q8_0(Vq, Vd, n / 32);
+    int rc = orc_attention_gqa(Q, Kd, Vd, O, H, Hkv, M, D, scale, o_token_major, nthreads);
+    free(Kd);
+    free(Vd);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm and RoPE of the MLX block (src/engine/model.py:17-48, :112-116,   */
+/* :215-226), restated in double with the fp16 rounding points of the model  */
+/* ------------------------------------------------------------------------ */
+
+/* RMSNorm over rows of X [M, D] (model.py:39-48):
+ *   normed = fp16(x / sqrt(mean(x^2) + eps))
+ *   y      = fp16(normed * w)               norm_type 1 ("rmsnorm")
+ *   y      = fp16(normed * fp16(1 + w))     norm_type 2 ("gemma_add_one")
+ * The mean and root are taken in double (the model: float32). */
+EXPORT int orc_rmsnorm(const uint16_t* X, const uint16_t* w, uint16_t* Y, uint32_t M, uint32_t D,
+                       float eps, int norm_type) {
+    if (norm_type != 1 && norm_type != 2) return -3;
+    for (uint32_t m = 0; m < M; m++) {
+        const uint16_t* x = X + (size_t)m * D;
+        double ss = 0.0;
+        for (uint32_t d = 0; d < D; d++) {
+            double v = orc_f16_to_f64(x[d]);
+            ss += v * v;
+        }
+        double r = 1.0 / sqrt(ss / (double)D + (double)eps);
+        for (uint32_t d = 0; d < D; d++) {
+            double nv = orc_f16_to_f64(orc_f64_to_f16(orc_f16_to_f64(x[d]) * r));
+            double wv = orc_f16_to_f64(w[d]);
+            if (norm_type == 2) wv = orc_f16_to_f64(orc_f64_to_f16(1.0 + wv));
+            Y[(size_t)m * D + d] = orc_f64_to_f16(nv * wv);
+        }
+    }
+    return 0;
+}
+
+/* Rotary position embedding in place on T [H, M, D] (nn.RoPE(dims = D,
+ * traditional, base = theta) at model.py:112-116, applied with the cache
+ * offset at :218-219).  Row m has position offset + m; pair i (0 <= i < D/2)
+ * rotates by angle pos * theta^(-2i/D): elements (i, i + D/2), or (2i, 2i+1)
+ * when traditional:  a' = a cos - b sin,  b' = a sin + b cos, each rounded to
+ * fp16 once. */
+EXPORT int orc_rope(uint16_t* T, uint32_t H, uint32_t M, uint32_t D, float theta, uint32_t offset,
+                    int traditional) {
+    if (D % 2) return -4;
+    uint32_t half = D / 2;
+    for (size_t r = 0; r < (size_t)H * M; r++) {
+        uint16_t* t = T + r * D;
+        double pos = (double)(offset + (uint32_t)(r % M));
+        for (uint32_t i = 0; i < half; i++) {
+            double ang = pos * pow((double)theta, -2.0 * (double)i / (double)D);
+            double c = cos(ang), sn = sin(ang);
+            uint32_t ia = traditional ? 2 * i : i, ib = traditional ? 2 * i + 1 : i + half;
+            double a = orc_f16_to_f64(t[ia]), b = orc_f16_to_f64(t[ib]);
+            t[ia] = orc_f64_to_f16(a * c - b * sn);
+            t[ib] = orc_f64_to_f16(a * sn + b * c);
+        }
+    }
+    return 0;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -596,5 +680,64 @@ EXPORT int orc_layer(int f, const uint16_t* X, const uint8_t* Wq, const uint8_t*
     if (!S) free(s);
     free(kq);
     free(vq);
+    return rc;
+}
+
+/*
+ * The MLX block with the router's projections (src/engine/model.py:181-265):
+ *   Xn    = RMSNorm(X, w_attn)                 (skipped when w_attn is NULL)
+ *   Q     = fp16(Xn . Wq^T) [Hq, M, D];  K, V = fp16(Xn . Wk/v^T) [Hkv, M, D]
+ *   Q, K  = RoPE(Q), RoPE(K) at positions offset + m   (skipped if !rope)
+ *   O     = fp16(causal_attn_gqa(Q, deq Q8_0(K), deq Q8_0(V))) token-major
+ *   Xmid  = fp16(X + O . Wo^T)
+ *   Xn2   = RMSNorm(Xmid, w_ffn)               (skipped when w_ffn is NULL)
+ *   S     = fp16(silu(Xn2 . Wg^T) * (Xn2 . Wu^T))
+ *   Xout  = fp16(Xmid + S . Wd^T)
+ * The KV cache is Q8_0 as in the router's layer (unified_prefill_engine.mm:
+ * 554-572); rounding points are those of the GPU pipeline.
+ */
+EXPORT int orc_layer_ex(int f, const uint16_t* X, const uint16_t* w_attn, const uint8_t* Wq,
+                        const uint8_t* Wk, const uint8_t* Wv, const uint8_t* Wo, const uint16_t* w_ffn,
+                        const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd, uint16_t* Xout,
+                        uint32_t M, uint32_t dm, uint32_t Hq, uint32_t Hkv, uint32_t D, uint32_t Nm,
+                        float scale, int norm_type, float eps, int rope, float theta, uint32_t offset,
+                        int traditional, int nthreads) {
+    if (!Hkv || Hq % Hkv) return -4;
+    uint32_t HQ = Hq * D, HK = Hkv * D;
+    size_t nq = (size_t)M * HQ, nk = (size_t)M * HK;
+    uint16_t* xn = (uint16_t*)malloc((size_t)M * dm * 2);
+    uint16_t* q = (uint16_t*)malloc(nq * 2);
+    uint16_t* k = (uint16_t*)malloc(nk * 2);
+    uint16_t* v = (uint16_t*)malloc(nk * 2);
+    uint16_t* o = (uint16_t*)malloc(nq * 2);
+    uint16_t* xm = (uint16_t*)malloc((size_t)M * dm * 2);
+    uint16_t* s = (uint16_t*)malloc((size_t)M * Nm * 2);
+    uint8_t* kq = (uint8_t*)malloc(nk / 32 * 34);
+    uint8_t* vq = (uint8_t*)malloc(nk / 32 * 34);
+    int rc = 0;
+    const uint16_t* a = X;
+    if (w_attn) {
+        rc |= orc_rmsnorm(X, w_attn, xn, M, dm, eps, norm_type);
+        a = xn;
+    }
+    rc |= orc_gemm(f, a, Wq, q, NULL, M, HQ, dm, 1, Hq, D, nthreads);
+    rc |= orc_gemm(f, a, Wk, k, NULL, M, HK, dm, 1, Hkv, D, nthreads);
+    rc |= orc_gemm(f, a, Wv, v, NULL, M, HK, dm, 1, Hkv, D, nthreads);
+    if (rope) {
+        rc |= orc_rope(q, Hq, M, D, theta, offset, traditional);
+        rc |= orc_rope(k, Hkv, M, D, theta, offset, traditional);
+    }
+    orc_quantize_q8_0(k, kq, nk / 32);
+    orc_quantize_q8_0(v, vq, nk / 32);
+    rc |= orc_attention_q8_0_gqa(q, kq, vq, o, Hq, Hkv, M, D, scale, 1, nthreads);
+    rc |= orc_gemm(f, o, Wo, xm, X, M, dm, HQ, 0, 0, 0, nthreads);
+    a = xm;
+    if (w_ffn) {
+        rc |= orc_rmsnorm(xm, w_ffn, xn, M, dm, eps, norm_type);
+        a = xn;
+    }
+    rc |= orc_swiglu(f, a, Wg, Wu, s, M, Nm, dm, nthreads);
+    rc |= orc_gemm(f, s, Wd, Xout, xm, M, dm, Nm, 0, 0, 0, nthreads);
+    free(xn); free(q); free(k); free(v); free(o); free(xm); free(s); free(kq); free(vq);
     return rc;
 }

@@ -51,6 +51,16 @@ def lib() -> ctypes.CDLL:
         L.orc_attention_q8_0.argtypes = [vp, vp, vp, vp, u32, u32, u32, f, i, i]
         L.orc_layer.argtypes = [i] + [vp] * 9 + [u32, u32, u32, u32, u32, f] + [vp] * 6 + [i]
         L.orc_layer.restype = i
+        L.orc_attention_gqa.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, f, i, i]
+        L.orc_attention_gqa.restype = i
+        L.orc_attention_q8_0_gqa.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, f, i, i]
+        L.orc_attention_q8_0_gqa.restype = i
+        L.orc_rmsnorm.argtypes = [vp, vp, vp, u32, u32, f, i]
+        L.orc_rmsnorm.restype = i
+        L.orc_rope.argtypes = [vp, u32, u32, u32, f, u32, i]
+        L.orc_rope.restype = i
+        L.orc_layer_ex.argtypes = [i] + [vp] * 11 + [u32] * 6 + [f, i, f, i, f, u32, i, i]
+        L.orc_layer_ex.restype = i
         _lib = L
     return _lib
 
@@ -178,3 +188,63 @@ def layer(fmt: int, X, Wq, Wk, Wv, Wo, Wg, Wu, Wd, H: int, D: int, N_mlp: int, s
                          nthreads or threads())
     assert rc == 0, rc
     return (out, inter) if intermediates else out
+
+
+def attention_gqa(Q, K, V, scale: float, o_token_major: bool = False, nthreads: int | None = None):
+    """Q [H, M, D], K/V [Hkv, M, D]: query head h reads KV head h // (H // Hkv)."""
+    Q, K, V = (np.ascontiguousarray(a, dtype=np.float16) for a in (Q, K, V))
+    H, M, D = Q.shape
+    out = np.empty((M, H * D) if o_token_major else (H, M, D), np.float16)
+    rc = lib().orc_attention_gqa(_p(Q), _p(K), _p(V), _p(out), H, K.shape[0], M, D, scale, int(o_token_major),
+                                 nthreads or threads())
+    assert rc == 0, rc
+    return out
+
+
+def attention_q8_0_gqa(Q, Kq, Vq, Hkv: int, scale: float, o_token_major: bool = False,
+                       nthreads: int | None = None):
+    Q = np.ascontiguousarray(Q, dtype=np.float16)
+    H, M, D = Q.shape
+    Kq = np.ascontiguousarray(Kq, dtype=np.uint8)
+    Vq = np.ascontiguousarray(Vq, dtype=np.uint8)
+    out = np.empty((M, H * D) if o_token_major else (H, M, D), np.float16)
+    rc = lib().orc_attention_q8_0_gqa(_p(Q), _p(Kq), _p(Vq), _p(out), H, Hkv, M, D, scale, int(o_token_major),
+                                      nthreads or threads())
+    assert rc == 0, rc
+    return out
+
+
+def rmsnorm(X, w, eps: float = 1e-5, norm_type: int = 1) -> np.ndarray:
+    X = np.ascontiguousarray(X, dtype=np.float16)
+    w = np.ascontiguousarray(w, dtype=np.float16)
+    M, D = X.shape
+    out = np.empty_like(X)
+    rc = lib().orc_rmsnorm(_p(X), _p(w), _p(out), M, D, eps, norm_type)
+    assert rc == 0, rc
+    return out
+
+
+def rope(T, theta: float = 10000.0, offset: int = 0, traditional: bool = False) -> np.ndarray:
+    """RoPE of T [H, M, D] (returns a new array)."""
+    T = np.array(T, dtype=np.float16, copy=True, order="C")
+    H, M, D = T.shape
+    rc = lib().orc_rope(_p(T), H, M, D, theta, offset, int(traditional))
+    assert rc == 0, rc
+    return T
+
+
+def layer_ex(fmt: int, X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, Hq: int, Hkv: int, D: int, N_mlp: int,
+             scale: float, norm_type: int = 1, eps: float = 1e-5, rope: bool = True, theta: float = 10000.0,
+             offset: int = 0, traditional: bool = False, nthreads: int | None = None) -> np.ndarray:
+    X = np.ascontiguousarray(X, dtype=np.float16)
+    M, dm = X.shape
+    na = None if w_attn is None else np.ascontiguousarray(w_attn, dtype=np.float16)
+    nf = None if w_ffn is None else np.ascontiguousarray(w_ffn, dtype=np.float16)
+    Ws = [np.ascontiguousarray(w, dtype=np.uint8) for w in (Wq, Wk, Wv, Wo, Wg, Wu, Wd)]
+    out = np.empty((M, dm), np.float16)
+    rc = lib().orc_layer_ex(fmt, _p(X), _p(na) if na is not None else None, *[_p(w) for w in Ws[:4]],
+                            _p(nf) if nf is not None else None, *[_p(w) for w in Ws[4:]], _p(out), M, dm, Hq, Hkv,
+                            D, N_mlp, scale, norm_type, eps, int(rope), theta, offset, int(traditional),
+                            nthreads or threads())
+    assert rc == 0, rc
+    return out

@@ -504,3 +504,89 @@ def test_gguf_q4_k_tensor_feeds_the_projection(bridge, oracle):
     bridge.synchronize()
     ref = oracle.gemm(2, X, W, N)
     tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, 2, X, W, K, N), K))
+
+
+# --------------------------------------------------------------------------
+# MLX block extras: RMSNorm, RoPE, grouped-query attention, full block
+# --------------------------------------------------------------------------
+
+def ulps16(a, b):
+    """Distance in binary16 steps between two fp16 arrays of the same sign pattern."""
+    ia = np.asarray(a, np.float16).view(np.int16).astype(np.int32)
+    ib = np.asarray(b, np.float16).view(np.int16).astype(np.int32)
+    ia = np.where(ia < 0, -32768 - ia, ia)
+    ib = np.where(ib < 0, -32768 - ib, ib)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("norm_type", [1, 2])
+@pytest.mark.parametrize("M,D", [(1, 64), (37, 2048), (130, 4096), (8, 8)])
+def test_rmsnorm(bridge, oracle, norm_type, M, D):
+    """fp16(fp16(x r) w): the GPU forms r in fp32, the oracle in double, so
+    x r near an fp16 tie may land one step away, which the exact product with
+    w carries into at most two output steps; everything else is exact."""
+    rng = np.random.default_rng(M + D)
+    X = (rng.standard_normal((M, D)) * 3).astype(np.float16)
+    w = (rng.standard_normal(D) * (0.1 if norm_type == 2 else 1.0)).astype(np.float16)
+    Y = empty16(M, D)
+    bridge.rmsnorm(dev(X), dev(w), Y, eps=1e-5, norm_type=norm_type)
+    bridge.synchronize()
+    ref = oracle.rmsnorm(X, w, eps=1e-5, norm_type=norm_type)
+    u = ulps16(host(Y), ref)
+    assert u.max() <= 2 and (u > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("traditional", [False, True])
+@pytest.mark.parametrize("H,M,D,offset", [(2, 33, 64, 0), (4, 300, 128, 4000), (1, 2048, 64, 0)])
+def test_rope(bridge, oracle, traditional, H, M, D, offset):
+    rng = np.random.default_rng(H * M + D)
+    T = (rng.standard_normal((H, M, D)) * 2).astype(np.float16)
+    t = dev(T)
+    bridge.rope(t, theta=10000.0, offset=offset, traditional=traditional)
+    bridge.synchronize()
+    ref = oracle.rope(T, theta=10000.0, offset=offset, traditional=traditional)
+    # one fp16 step of the result, plus the fp32 rotation error (a few 2^-24 of
+    # the pair's magnitude), which matters only where a cos - b sin cancels
+    d = np.abs(host(t).astype(np.float64) - ref.astype(np.float64))
+    step = np.spacing(np.abs(ref)).astype(np.float64)
+    assert np.all(d <= step + 2.0 ** -20 * float(np.abs(T).max()))
+    assert (d > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("H,Hkv,M,D", [(8, 2, 129, 64), (4, 1, 300, 128), (6, 3, 64, 64)])
+def test_flash_attention_gqa(bridge, oracle, H, Hkv, M, D):
+    rng = np.random.default_rng(H * Hkv + M)
+    Q = (rng.standard_normal((H, M, D)) * 0.5).astype(np.float16)
+    K, V = ((rng.standard_normal((Hkv, M, D)) * 0.5).astype(np.float16) for _ in range(2))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    O = empty16(M, H * D)
+    bridge.dispatch_flash_attn_q8_0_gqa(dev(Q), dev(Kq), dev(Vq), O, H, Hkv, M, D, scale, o_token_major=True)
+    bridge.synchronize()
+    ref = oracle.attention_q8_0_gqa(Q, Kq, Vq, Hkv, scale, o_token_major=True)
+    assert maxdiff(host(O), ref) <= TOL
+
+
+@pytest.mark.parametrize("norm_type,rope,traditional,Hkv", [(1, True, False, 2), (2, True, True, 4),
+                                                            (1, False, False, 1)])
+def test_prefill_layer_ex(bridge, oracle, norm_type, rope, traditional, Hkv):
+    M, dm, Hq, D, Nm = 160, 256, 4, 64, 512
+    X = synth.activations(M, dm, 71)
+    w_attn = (1 + 0.1 * np.random.default_rng(72).standard_normal(dm)).astype(np.float16)
+    w_ffn = (1 + 0.1 * np.random.default_rng(73).standard_normal(dm)).astype(np.float16)
+    if norm_type == 2:
+        w_attn, w_ffn = (w_attn - 1).astype(np.float16), (w_ffn - 1).astype(np.float16)
+    shapes = [(Hq * D, dm), (Hkv * D, dm), (Hkv * D, dm), (dm, Hq * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    Ws = [synth.quantized_weights(0, n, k, 80 + i) for i, (n, k) in enumerate(shapes)]
+    out = empty16(M, dm)
+    bridge.prefill_layer_ex(dev(X), dev(w_attn), *[dev(w) for w in Ws[:4]], dev(w_ffn), *[dev(w) for w in Ws[4:]], out,
+                            0, M, dm, Hq, Hkv, D, Nm, 0.125, norm_type=norm_type, norm_eps=1e-5, rope=rope,
+                            rope_theta=10000.0, rope_offset=17, rope_traditional=traditional)
+    bridge.synchronize()
+    ref = oracle.layer_ex(0, X, w_attn, *Ws[:4], w_ffn, *Ws[4:], Hq, Hkv, D, Nm, 0.125, norm_type=norm_type,
+                          eps=1e-5, rope=rope, theta=10000.0, offset=17, traditional=traditional)
+    d = maxdiff(host(out), ref)
+    print(f"layer_ex max|diff| = {d}")
+    # fp16 intermediates on both sides; a tie flipped upstream (norm, RoPE) moves
+    # a downstream value by about one output step
+    assert d <= 2 * TOL

@@ -452,3 +452,77 @@ def test_q8_0_weights_match_kv_dequantizer(oracle):
     q = oracle.quantize_q8_0(x)
     np.testing.assert_array_equal(oracle.dequantize(6, q, 64 * 32, 1).reshape(-1).view(np.uint16),
                                   oracle.dequantize_q8_0(q).reshape(-1).view(np.uint16))
+
+
+# --------------------------------------------------------------------------
+# RMSNorm / RoPE / grouped-query attention of the MLX block
+# (src/engine/model.py:17-48, :112-116, :215-236)
+# --------------------------------------------------------------------------
+
+def test_rmsnorm_closed_forms(oracle):
+    # x = (3, 4): mean square 12.5, normed = x / sqrt(12.5 + eps)
+    x = np.array([[3.0, 4.0]], np.float16)
+    w = np.array([1.0, -2.0], np.float16)
+    r = 1.0 / np.sqrt(12.5 + 1e-5)
+    expect = np.float16(np.float16(np.array([3.0, 4.0]) * r) * np.array([1.0, -2.0]))
+    np.testing.assert_array_equal(oracle.rmsnorm(x, w), expect[None, :])
+    # a row of ones returns w (1 / sqrt(1 + 1e-5) rounds to 1 in fp16)
+    w = np.random.default_rng(0).standard_normal(64).astype(np.float16)
+    np.testing.assert_array_equal(oracle.rmsnorm(np.ones((3, 64), np.float16), w), np.tile(w, (3, 1)))
+    # gemma_add_one with w = 0 is the plain normalisation; scale invariance of the normalised row
+    x = np.random.default_rng(1).standard_normal((4, 256)).astype(np.float16)
+    z = np.zeros(256, np.float16)
+    a = oracle.rmsnorm(x, z, eps=0.0, norm_type=2).astype(np.float64)
+    b = oracle.rmsnorm((x.astype(np.float64) * 4).astype(np.float16), z, eps=0.0, norm_type=2).astype(np.float64)
+    np.testing.assert_array_equal(a, b)  # x * 4 is exact in fp16
+    np.testing.assert_allclose((a ** 2).mean(1), 1.0, rtol=2e-3)
+
+
+def test_rope_closed_forms(oracle):
+    # theta = 10000, D = 4, position 1: pair (0, 2) rotates by 1 rad, pair (1, 3) by 0.01 rad
+    x = np.zeros((1, 1, 4), np.float16)
+    x[0, 0, 0] = 1.0
+    x[0, 0, 1] = 1.0
+    y = oracle.rope(x, offset=1).astype(np.float64)[0, 0]
+    np.testing.assert_array_equal(y, np.float16([np.cos(1.0), np.cos(0.01), np.sin(1.0), np.sin(0.01)]))
+    # position 0 is the identity; offset shifts positions
+    T = np.random.default_rng(2).standard_normal((3, 5, 64)).astype(np.float16)
+    np.testing.assert_array_equal(oracle.rope(T[:, :1]), T[:, :1])
+    np.testing.assert_array_equal(oracle.rope(T, offset=7)[:, 1:], oracle.rope(np.concatenate([T[:, :1], T], 1),
+                                                                                  offset=6)[:, 2:])
+    # rotations keep each pair's norm (to fp16 rounding)
+    y = oracle.rope(T, offset=100).astype(np.float64)
+    n0 = T.astype(np.float64)[..., :32] ** 2 + T.astype(np.float64)[..., 32:] ** 2
+    n1 = y[..., :32] ** 2 + y[..., 32:] ** 2
+    np.testing.assert_allclose(n1, n0, rtol=4e-3, atol=1e-3)
+    # traditional pairs (2i, 2i+1) == split-half pairs (i, i + D/2) under the interleave permutation
+    perm = np.concatenate([np.arange(0, 64, 2), np.arange(1, 64, 2)])
+    yt = oracle.rope(T, offset=3, traditional=True)
+    ys = oracle.rope(T[..., perm], offset=3, traditional=False)
+    np.testing.assert_array_equal(yt[..., perm], ys)
+
+
+def test_grouped_query_attention_is_repeated_kv(oracle):
+    rng = np.random.default_rng(3)
+    H, Hkv, M, D = 4, 2, 40, 64
+    Q = rng.standard_normal((H, M, D)).astype(np.float16)
+    K = rng.standard_normal((Hkv, M, D)).astype(np.float16)
+    V = rng.standard_normal((Hkv, M, D)).astype(np.float16)
+    a = oracle.attention_gqa(Q, K, V, 0.125)
+    b = oracle.attention(Q, np.repeat(K, H // Hkv, axis=0), np.repeat(V, H // Hkv, axis=0), 0.125)
+    np.testing.assert_array_equal(a, b)
+    a1 = oracle.attention_gqa(Q, K[:1], V[:1], 0.125, o_token_major=True)
+    b1 = oracle.attention(Q, np.repeat(K[:1], H, 0), np.repeat(V[:1], H, 0), 0.125, o_token_major=True)
+    np.testing.assert_array_equal(a1, b1)
+
+
+def test_layer_ex_reduces_to_the_router_layer(oracle):
+    """No norms, no RoPE and Hkv = H: the MLX-block layer is the router layer."""
+    rng = np.random.default_rng(4)
+    M, dm, H, D, Nm = 24, 256, 4, 64, 256
+    X = (rng.standard_normal((M, dm)) * 0.5).astype(np.float16)
+    W = [synth.quantized_weights(0, n, k, 10 + i) for i, (n, k) in
+         enumerate([(H * D, dm), (H * D, dm), (H * D, dm), (dm, H * D), (Nm, dm), (Nm, dm), (dm, Nm)])]
+    a = oracle.layer(0, X, *W, H, D, Nm, 0.125)
+    b = oracle.layer_ex(0, X, None, *W[:4], None, *W[4:], H, H, D, Nm, 0.125, rope=False)
+    np.testing.assert_array_equal(a, b)
