@@ -216,6 +216,69 @@ def bench_layer(b, timer, M, dm, H, D, Nm, seed):
             "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
 
 
+def bench_layer_ex(b, timer, M, dm, Hq, Hkv, D, Nm, seed):
+    """The full Llama-3.2-1B block (RMSNorm, RoPE, grouped-query attention with
+    Hkv = 8, Q4_0 weights, Q8_0 KV) through m4_bridge_prefill_layer_ex."""
+    import torch
+
+    import synth
+
+    X = torch.from_numpy(synth.activations(M, dm, seed)).cuda()
+    shapes = [(Hq * D, dm), (Hkv * D, dm), (Hkv * D, dm), (dm, Hq * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    Ws = [torch.from_numpy(synth.quantized_weights(0, n, k, seed + 1 + i)).cuda() for i, (n, k) in enumerate(shapes)]
+    na = torch.ones(dm, dtype=torch.float16, device="cuda")
+    nf = torch.ones(dm, dtype=torch.float16, device="cuda")
+    Xo = torch.empty(M, dm, dtype=torch.float16, device="cuda")
+    lib = b.lib
+    ptrs = ([X.data_ptr(), na.data_ptr()] + [w.data_ptr() for w in Ws[:4]] + [nf.data_ptr()] +
+            [w.data_ptr() for w in Ws[4:]] + [Xo.data_ptr()])
+
+    def step(i):
+        check(lib.m4_bridge_prefill_layer_ex(*ptrs, 0, M, dm, Hq, Hkv, D, Nm, 1.0 / math.sqrt(D), 1, 1e-5, 1,
+                                             500000.0, 0, 0), "layer_ex")
+
+    ms = timer.run(step)
+    flops = (2.0 * M * dm * (Hq + 2 * Hkv) * D + 2.0 * M * Hq * D * dm + 2.0 * M * dm * Nm * 3 +
+             2.0 * Hq * M * (M + 1) * D)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"name": "block_llama32_1b_gqa8_rmsnorm_rope", "M": M, "d_model": dm, "Hq": Hq, "Hkv": Hkv, "D": D,
+            "N_mlp": Nm, "ms": round(ms, 5), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4),
+            "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
+
+
+def bench_rmsnorm(b, timer, M, D, seed):
+    import torch
+
+    X = torch.randn(M, D, dtype=torch.float16, device="cuda")
+    w = torch.ones(D, dtype=torch.float16, device="cuda")
+    Y = torch.empty_like(X)
+    lib = b.lib
+    args = (X.data_ptr(), X.numel() * 2, w.data_ptr(), D * 2, Y.data_ptr(), Y.numel() * 2, M, D, 1e-5, 1)
+
+    def step(i):
+        check(lib.m4_bridge_rmsnorm(*args), "rmsnorm")
+
+    ms = timer.run(step)
+    gbs = (2.0 * M * D * 2 + D * 2) / (ms * 1e-3) / 1e9
+    return {"name": "rmsnorm", "M": M, "D": D, "ms": round(ms, 5), "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "timing": timer.mode}
+
+
+def bench_rope(b, timer, H, M, D, seed):
+    import torch
+
+    T = torch.randn(H, M, D, dtype=torch.float16, device="cuda")
+    lib = b.lib
+
+    def step(i):
+        check(lib.m4_bridge_rope(T.data_ptr(), T.numel() * 2, H, M, D, 500000.0, 0, 0), "rope")
+
+    ms = timer.run(step)
+    gbs = 2.0 * T.numel() * 2 / (ms * 1e-3) / 1e9
+    return {"name": "rope", "H": H, "M": M, "D": D, "ms": round(ms, 5), "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "timing": timer.mode}
+
+
 def bench_fp16_reference(timer, name, M, K, N):
     """Calibration point, not a router kernel: the vendor library's unquantized
     fp16 GEMM (torch.matmul -> hipBLASLt) of the same shape, weights rotated the
@@ -335,6 +398,12 @@ def main():
         per["cfg5_attention"] = bench_attention(b, timer, 32, 2048, 64, 51)
     if on("cfg5_layer"):
         per["cfg5_layer"] = bench_layer(b, timer, 2048, 2048, 32, 64, 8192, 52)
+    if on("block_full"):
+        per["block_full"] = bench_layer_ex(b, timer, 2048, 2048, 32, 8, 64, 8192, 53)
+    if on("rmsnorm"):
+        per["rmsnorm"] = bench_rmsnorm(b, timer, 2048, 2048, 54)
+    if on("rope"):
+        per["rope"] = bench_rope(b, timer, 32, 2048, 64, 55)
 
     head = per.get("cfg2_mlx_m128") or next(iter(per.values()))
     traffic = traffic_from_profile("cfg2_mlx_m128") if "cfg2_mlx_m128" in per else None

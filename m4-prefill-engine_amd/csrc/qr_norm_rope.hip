@@ -8,7 +8,9 @@
 namespace qr {
 
 // One wave per row; each lane owns 8-element chunks lane, lane + 64, ...
-// Sum of squares in fp32, butterfly-reduced across the wave.
+// Rows of up to 64 * 8 * CPL elements stay in registers between the sum of
+// squares and the scaling (one HBM read); CPL = 0 streams the row twice.
+template <int CPL>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const _Float16* X, const _Float16* w, _Float16* Y, uint32_t M,
                                                       uint32_t D, float eps, int gemma) {
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -16,17 +18,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const _Float16* X, const _
     if (row >= M) return;
     const _Float16* x = X + (size_t)row * D;
     const uint32_t chunks = D / 8;
-    float ss = 0.0f;
-    for (uint32_t c = lane; c < chunks; c += 64) {
-        const h8_t v = *reinterpret_cast<const h8_t*>(x + 8 * c);
-#pragma unroll
-        for (int i = 0; i < 8; i++) ss = __builtin_fmaf((float)v[i], (float)v[i], ss);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
-    for (uint32_t c = lane; c < chunks; c += 64) {
-        const h8_t v = *reinterpret_cast<const h8_t*>(x + 8 * c);
+    auto scale_store = [&](uint32_t c, const h8_t& v, float r) {
         const h8_t wv = *reinterpret_cast<const h8_t*>(w + 8 * c);
         h8_t o;
 #pragma unroll
@@ -36,6 +28,37 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const _Float16* X, const _
             o[i] = (_Float16)((float)nv * (float)ww);  // exact product, one rounding
         }
         *reinterpret_cast<h8_t*>(Y + (size_t)row * D + 8 * c) = o;
+    };
+    float ss = 0.0f;
+    h8_t keep[CPL > 0 ? CPL : 1];
+    if constexpr (CPL > 0) {
+#pragma unroll
+        for (int k = 0; k < CPL; k++) {
+            const uint32_t c = lane + 64 * k;
+            keep[k] = c < chunks ? *reinterpret_cast<const h8_t*>(x + 8 * c) : h8_t{};
+        }
+#pragma unroll
+        for (int k = 0; k < CPL; k++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss = __builtin_fmaf((float)keep[k][i], (float)keep[k][i], ss);
+    } else {
+        for (uint32_t c = lane; c < chunks; c += 64) {
+            const h8_t v = *reinterpret_cast<const h8_t*>(x + 8 * c);
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss = __builtin_fmaf((float)v[i], (float)v[i], ss);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    if constexpr (CPL > 0) {
+#pragma unroll
+        for (int k = 0; k < CPL; k++) {
+            const uint32_t c = lane + 64 * k;
+            if (c < chunks) scale_store(c, keep[k], r);
+        }
+    } else {
+        for (uint32_t c = lane; c < chunks; c += 64) scale_store(c, *reinterpret_cast<const h8_t*>(x + 8 * c), r);
     }
 }
 
@@ -66,13 +89,16 @@ __global__ void __launch_bounds__(256) rope_kernel(_Float16* T, uint32_t rows, u
 #pragma unroll
         for (int k = 0; k < 8; k++) { a[k] = (float)u[k]; b[k] = (float)v[k]; }
     }
+    // inverse frequency of pair i0, then successive ratios theta^(-2/D)
     const double l2t = log2((double)theta);
-    const double two_pi = 6.283185307179586476925286766559;
+    const double ratio = exp2(-2.0 / (double)D * l2t);
+    double f = exp2(-2.0 * (double)i0 / (double)D * l2t);
+    const double two_pi = 6.283185307179586476925286766559, inv_two_pi = 0.15915494309189533576888376337251;
     float ra[8], rb[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const double ang = pos * exp2(-2.0 * (double)(i0 + k) / (double)D * l2t);
-        const float red = (float)(ang - two_pi * rint(ang / two_pi));
+    for (int k = 0; k < 8; k++, f *= ratio) {
+        const double ang = pos * f;
+        const float red = (float)__builtin_fma(-two_pi, rint(ang * inv_two_pi), ang);
         const float sn = sinf(red), cs = cosf(red);
         ra[k] = a[k] * cs - b[k] * sn;
         rb[k] = a[k] * sn + b[k] * cs;
@@ -98,7 +124,13 @@ __global__ void __launch_bounds__(256) rope_kernel(_Float16* T, uint32_t rows, u
 hipError_t launch_rmsnorm(const _Float16* X, const _Float16* w, _Float16* Y, uint32_t M, uint32_t D, float eps,
                           int norm_type, hipStream_t st) {
     if (D % 8 || (norm_type != 1 && norm_type != 2)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((M + 3) / 4), dim3(256), 0, st, X, w, Y, M, D, eps, norm_type == 2);
+    const dim3 grid((M + 3) / 4);
+    if (D <= 64 * 8 * 4)
+        hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, st, X, w, Y, M, D, eps, norm_type == 2);
+    else if (D <= 64 * 8 * 16)
+        hipLaunchKernelGGL(rmsnorm_kernel<16>, grid, dim3(256), 0, st, X, w, Y, M, D, eps, norm_type == 2);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<0>, grid, dim3(256), 0, st, X, w, Y, M, D, eps, norm_type == 2);
     return hipGetLastError();
 }
 
