@@ -18,6 +18,8 @@
 //    the matching key order in the V^T A-operand reads (two ds_read_b64).
 //  * fp32 running max / sum / output accumulators (the reference keeps
 //    S, P and O in half); the output is rounded to fp16 once.
+#include <type_traits>
+
 #include "qr_device.h"
 #include "qr_kernels.h"
 
@@ -29,37 +31,49 @@ namespace qr {
 // zero) with the UNROUNDED d, clamped to [-128, 127] (unified_kernels.metal:
 // 118-145).  One thread per block.
 // --------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) quantize_q8_0_kernel(const _Float16* src, uint8_t* dst, size_t nblocks) {
-    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (b >= nblocks) return;
-    const u4_t* s = reinterpret_cast<const u4_t*>(src + b * 32);
-    uint32_t w[16];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        u4_t v = s[i];
-        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-    }
-    float x[32];
+// One block: x[32] -> half(d) bits and 16 code words (two int8 codes each).
+__device__ __forceinline__ void quantize_block_q8_0(const float x[32], uint32_t& d16, uint32_t codes[16]) {
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        x[2 * i] = h2f(w[i] & 0xffffu);
-        x[2 * i + 1] = h2f(w[i] >> 16);
-        amax = fmaxf(amax, fabsf(x[2 * i]));
-        amax = fmaxf(amax, fabsf(x[2 * i + 1]));
-    }
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    uint16_t* o16 = reinterpret_cast<uint16_t*>(dst + b * 34);  // 34-byte blocks are 2-byte aligned
-    o16[0] = (uint16_t)f2h_bits(d);
+    d16 = f2h_bits(d);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         int q0 = (int)__builtin_roundf(x[2 * i] * id);
         int q1 = (int)__builtin_roundf(x[2 * i + 1] * id);
         q0 = q0 < -128 ? -128 : (q0 > 127 ? 127 : q0);
         q1 = q1 < -128 ? -128 : (q1 > 127 ? 127 : q1);
-        o16[1 + i] = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+        codes[i] = (uint32_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
     }
+}
+
+__device__ __forceinline__ void load_block_f16(const _Float16* src, float x[32]) {
+    const u4_t* s = reinterpret_cast<const u4_t*>(src);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u4_t v = s[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            x[8 * i + 2 * k] = h2f(w[k] & 0xffffu);
+            x[8 * i + 2 * k + 1] = h2f(w[k] >> 16);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) quantize_q8_0_kernel(const _Float16* src, uint8_t* dst, size_t nblocks) {
+    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblocks) return;
+    float x[32];
+    load_block_f16(src + b * 32, x);
+    uint32_t d16, codes[16];
+    quantize_block_q8_0(x, d16, codes);
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(dst + b * 34);  // 34-byte blocks are 2-byte aligned
+    o16[0] = (uint16_t)d16;
+#pragma unroll
+    for (int i = 0; i < 16; i++) o16[1 + i] = (uint16_t)codes[i];
 }
 
 hipError_t launch_quantize_q8_0(const _Float16* src, uint8_t* dst, size_t nblocks, hipStream_t st) {
@@ -197,6 +211,107 @@ __device__ __forceinline__ void attn_stage(const AttnRaw<D>& raw, int k0, int ti
     }
 }
 
+// Staging from a dequantized fp16 cache: K' [H, Mp, D] (row-major) and V'^T
+// [H, D, Mp] (keys contiguous per dim), Mp = M rounded up to whole 64-key
+// tiles.  Both LDS tiles are then plain 16-byte copies: no per-tile decode.
+template <int D>
+struct AttnRawF16 {
+    static constexpr int CH = D / 32;  // 16-byte chunks per thread for each of K and V^T
+    u4_t k[CH];
+    u4_t v[CH];
+};
+
+template <int D>
+__device__ __forceinline__ void attn_fetch_f16(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int k0, int Mp,
+                                               int tid, AttnRawF16<D>& raw) {
+#pragma unroll
+    for (int i = 0; i < AttnRawF16<D>::CH; i++) {
+        const int c = tid + 256 * i;
+        const int key = c / (D / 8), kc = c % (D / 8);        // K: 64 keys x D/8 chunks
+        raw.k[i] = ld_b128(kr, (uint32_t)((k0 + key) * D + kc * 8) * 2u);
+        const int d = c / 8, vc = c % 8;                        // V^T: D rows x 8 chunks of 8 keys
+        raw.v[i] = ld_b128(vr, (uint32_t)(d * Mp + k0 + vc * 8) * 2u);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void attn_stage_f16(const AttnRawF16<D>& raw, int tid, _Float16* Ks, _Float16* Vt) {
+    constexpr int KROW = D + 8, VROW = kBKV + 8;
+#pragma unroll
+    for (int i = 0; i < AttnRawF16<D>::CH; i++) {
+        const int c = tid + 256 * i;
+        *reinterpret_cast<u4_t*>(Ks + (c / (D / 8)) * KROW + (c % (D / 8)) * 8) = raw.k[i];
+        *reinterpret_cast<u4_t*>(Vt + (c / 8) * VROW + (c % 8) * 8) = raw.v[i];
+    }
+}
+
+// Dequantized fp16 cache for the attention kernel, one workgroup per 64-key
+// tile of one head.  FROM_Q8: from Q8_0 blocks (half(q * half(d)), the
+// reference's dequantizer, brick4_attn_bench.mm:57-65); otherwise from fp16
+// K / V through the same quantize-then-dequantize arithmetic as
+// quantize_q8_0_kernel + the Q8_0 path (bit-identical values, no Q8_0 buffer
+// written).  K' rows go straight out; V' is transposed through LDS so V'^T
+// rows leave as 128-byte runs.  Keys M .. Mp - 1 are zero.
+template <int D, bool FROM_Q8>
+__global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const void* Vsrc, _Float16* Kf, _Float16* Vtf,
+                                                      uint32_t M, uint32_t Mp) {
+    constexpr int NB = D / 32;            // blocks per key
+    constexpr int TR = kBKV + 8;          // LDS row (halfs) of the transposed tile
+    __shared__ __attribute__((aligned(16))) _Float16 T[D * TR];
+    const int tid = threadIdx.x;
+    const uint32_t k0 = blockIdx.x * kBKV, hk = blockIdx.y;
+    const size_t head_src = (size_t)M * D, head_dst = (size_t)Mp * D;
+    for (int u = tid; u < 2 * kBKV * NB; u += 256) {
+        const bool isv = u >= kBKV * NB;
+        const int uu = isv ? u - kBKV * NB : u;
+        const int key = uu % kBKV, db = uu / kBKV;
+        const uint32_t gk = k0 + key;
+        uint32_t w[16];  // 32 dequantized halfs
+        if (gk < M) {
+            const size_t blk = hk * (head_src / 32) + (size_t)gk * NB + db;
+            uint32_t d16, codes[16];
+            if constexpr (FROM_Q8) {
+                const uint8_t* b = static_cast<const uint8_t*>(isv ? Vsrc : Ksrc) + blk * 34;
+                const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b);  // 2-byte aligned
+                d16 = b16[0];
+#pragma unroll
+                for (int i = 0; i < 16; i++) codes[i] = b16[1 + i];
+            } else {
+                float x[32];
+                load_block_f16(static_cast<const _Float16*>(isv ? Vsrc : Ksrc) + blk * 32, x);
+                quantize_block_q8_0(x, d16, codes);
+            }
+            const h2_t d = as_h2(d16 | (d16 << 16));
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t q = codes[2 * i] | (codes[2 * i + 1] << 16);
+                w[2 * i] = q8_pair<false>(q, d);
+                w[2 * i + 1] = q8_pair<true>(q, d);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) w[i] = 0u;
+        }
+        if (!isv) {
+            u4_t* dst = reinterpret_cast<u4_t*>(Kf + hk * head_dst + (size_t)gk * D + db * 32);
+#pragma unroll
+            for (int c = 0; c < 4; c++) dst[c] = u4_t{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                T[(db * 32 + 2 * i) * TR + key] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
+                T[(db * 32 + 2 * i + 1) * TR + key] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+            }
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c < D * 8; c += 256) {
+        const int d = c / 8, kc = c % 8;
+        *reinterpret_cast<u4_t*>(Vtf + hk * head_dst + (size_t)d * Mp + k0 + kc * 8) =
+            *reinterpret_cast<const u4_t*>(T + d * TR + kc * 8);
+    }
+}
+
 // Flash attention over a Q8_0 K/V cache (one workgroup = 4 wave64s = 128
 // queries of one head).
 //  * Each wave owns 32 queries and computes S^T = K . Q^T with
@@ -214,7 +329,7 @@ __device__ __forceinline__ void attn_stage(const AttnRaw<D>& raw, int k0, int ti
 //    8 keys that lane supplies as the B operand of O^T = V^T . P^T.
 //  * fp32 running max / sum / output accumulators (the reference keeps S, P
 //    and O in half); the output is rounded to fp16 once.
-template <int D>
+template <int D, bool F16>
 __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(AttnParams p) {
     using S = AttnStage<D>;
     constexpr int KROW = D + 8;                // LDS row (halfs) of K tile [key][d]
@@ -242,18 +357,35 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 
     const size_t head_elems = (size_t)M * D;
     const _Float16* Qh = p.Q + (size_t)h * head_elems;
-    const uint32_t kv_bytes = (uint32_t)(head_elems / 32 * 34);
     const int hk = p.Hkv ? h / ((int)p.H / (int)p.Hkv) : h;  // grouped-query: shared KV head
-    auto kr = make_rsrc(p.Kq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
-    auto vr = make_rsrc(p.Vq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
+    const int Mp = (int)p.Mp;
+    __amdgpu_buffer_rsrc_t kr, vr;
+    if constexpr (F16) {
+        const uint32_t bytes = (uint32_t)((size_t)Mp * D * 2);
+        kr = make_rsrc(p.Kf + (size_t)hk * Mp * D, bytes);
+        vr = make_rsrc(p.Vtf + (size_t)hk * Mp * D, bytes);
+    } else {
+        const uint32_t kv_bytes = (uint32_t)(head_elems / 32 * 34);
+        kr = make_rsrc(p.Kq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
+        vr = make_rsrc(p.Vq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
+    }
+    using Raw = typename std::conditional<F16, AttnRawF16<D>, AttnRaw<D>>::type;
+    auto fetch = [&](int k0, Raw& raw) {
+        if constexpr (F16) attn_fetch_f16<D>(kr, vr, k0, Mp, tid, raw);
+        else attn_fetch<D>(kr, vr, k0, M, tid, raw);
+    };
+    auto stage = [&](const Raw& raw, int k0, _Float16* Kd, _Float16* Vd) {
+        if constexpr (F16) attn_stage_f16<D>(raw, tid, Kd, Vd);
+        else attn_stage<D>(raw, k0, tid, Kd, Vd);
+    };
 
     const int q_last = min(q0 + kBQ, M) - 1;
     const int ntiles = q_last / kBKV + 1;
 
     // ---- prologue: tile 0 staged, tile 1 in flight ----
-    AttnRaw<D> rawA, rawB;
-    attn_fetch<D>(kr, vr, 0, M, tid, rawA);
-    if (ntiles > 1) attn_fetch<D>(kr, vr, kBKV, M, tid, rawB);
+    Raw rawA, rawB;
+    fetch(0, rawA);
+    if (ntiles > 1) fetch(kBKV, rawB);
 
     // Q^T fragments (B operand): lane holds Q[my_q][kk*16 + 8g .. +7].
     h8_t qf[D / 16];
@@ -266,7 +398,7 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
             qf[kk] = __builtin_bit_cast(h8_t, v);
         }
     }
-    attn_stage<D>(rawA, 0, tid, Ks[0], Vt[0]);
+    stage(rawA, 0, Ks[0], Vt[0]);
     __syncthreads();
 
     // scores -> log2 units: s * c with c > 0 (a negative scale flips the sign
@@ -287,17 +419,35 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
         if (k0 > qw + 31) return;  // whole tile above this wave's diagonal
         const _Float16* Kb = Ks[kt & 1];
         const _Float16* Vb = Vt[kt & 1];
-        // ---- S^T = K . Q^T : two 32-key tiles ----
+        // ---- S^T = K . Q^T : two 32-key tiles; all K fragments read first ----
+        h8_t ka[2][D / 16];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int kk = 0; kk < D / 16; kk++)
+                ka[ks][kk] = *reinterpret_cast<const h8_t*>(Kb + (ks * 32 + j) * KROW + kk * 16 + 8 * g);
         f16v_t s[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             s[ks] = f16v_t{};
 #pragma unroll
-            for (int kk = 0; kk < D / 16; kk++) {
-                h8_t a = *reinterpret_cast<const h8_t*>(Kb + (ks * 32 + j) * KROW + kk * 16 + 8 * g);
-                s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[ks], 0, 0, 0);
-            }
+            for (int kk = 0; kk < D / 16; kk++)
+                s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks][kk], qf[kk], s[ks], 0, 0, 0);
         }
+        // V^T fragments of the P.V step, read now so their latency hides under
+        // the softmax: step (ks, t2) needs keys 32ks + 16t2 + 4g + {0..3, 8..11}
+        u4_t va[2][2][DT];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int t = 0; t < DT; t++) {
+                    const _Float16* row = Vb + (t * 32 + j) * VROW + ks * 32 + t2 * 16 + 4 * g;
+                    const u2_t lo = *reinterpret_cast<const u2_t*>(row);
+                    const u2_t hi = *reinterpret_cast<const u2_t*>(row + 8);
+                    va[ks][t2][t] = u4_t{lo.x, lo.y, hi.x, hi.y};
+                }
         // ---- causal mask (diagonal tiles only), running max ----
         if (k0 + kBKV - 1 > qw) {
 #pragma unroll
@@ -345,29 +495,24 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
             for (int t2 = 0; t2 < 2; t2++) {
                 u4_t bw = {pk[ks][4 * t2], pk[ks][4 * t2 + 1], pk[ks][4 * t2 + 2], pk[ks][4 * t2 + 3]};
                 h8_t b = __builtin_bit_cast(h8_t, bw);
-                const int kb0 = ks * 32 + t2 * 16 + 4 * g;
 #pragma unroll
-                for (int t = 0; t < DT; t++) {
-                    const _Float16* row = Vb + (t * 32 + j) * VROW;
-                    u2_t lo = *reinterpret_cast<const u2_t*>(row + kb0);
-                    u2_t hi = *reinterpret_cast<const u2_t*>(row + kb0 + 8);
-                    u4_t aw = {lo.x, lo.y, hi.x, hi.y};
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, aw), b, o[t], 0, 0, 0);
-                }
+                for (int t = 0; t < DT; t++)
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[ks][t2][t]), b, o[t], 0,
+                                                                  0, 0);
             }
     };
 
     // ---- main loop, unrolled by two for the raw register sets:
     // iteration kt: fetch tile kt + 2, multiply tile kt, stage tile kt + 1 ----
     for (int kt = 0; kt < ntiles; kt += 2) {
-        if (kt + 2 < ntiles) attn_fetch<D>(kr, vr, (kt + 2) * kBKV, M, tid, rawA);
+        if (kt + 2 < ntiles) fetch((kt + 2) * kBKV, rawA);
         compute(kt);
-        if (kt + 1 < ntiles) attn_stage<D>(rawB, (kt + 1) * kBKV, tid, Ks[(kt + 1) & 1], Vt[(kt + 1) & 1]);
+        if (kt + 1 < ntiles) stage(rawB, (kt + 1) * kBKV, Ks[(kt + 1) & 1], Vt[(kt + 1) & 1]);
         __syncthreads();
         if (kt + 1 >= ntiles) break;
-        if (kt + 3 < ntiles) attn_fetch<D>(kr, vr, (kt + 3) * kBKV, M, tid, rawB);
+        if (kt + 3 < ntiles) fetch((kt + 3) * kBKV, rawB);
         compute(kt + 1);
-        if (kt + 2 < ntiles) attn_stage<D>(rawA, (kt + 2) * kBKV, tid, Ks[kt & 1], Vt[kt & 1]);
+        if (kt + 2 < ntiles) stage(rawA, (kt + 2) * kBKV, Ks[kt & 1], Vt[kt & 1]);
         __syncthreads();
     }
 
@@ -390,9 +535,33 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
+    const bool f16 = p.Kf != nullptr;
+    if (f16 && (p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV)) return hipErrorInvalidValue;
     switch (p.D) {
-        case 64: hipLaunchKernelGGL(flash_attn_q8_0_kernel<64>, grid, dim3(256), 0, st, p); break;
-        case 128: hipLaunchKernelGGL(flash_attn_q8_0_kernel<128>, grid, dim3(256), 0, st, p); break;
+        case 64:
+            if (f16) hipLaunchKernelGGL((flash_attn_q8_0_kernel<64, true>), grid, dim3(256), 0, st, p);
+            else hipLaunchKernelGGL((flash_attn_q8_0_kernel<64, false>), grid, dim3(256), 0, st, p);
+            break;
+        case 128:
+            if (f16) hipLaunchKernelGGL((flash_attn_q8_0_kernel<128, true>), grid, dim3(256), 0, st, p);
+            else hipLaunchKernelGGL((flash_attn_q8_0_kernel<128, false>), grid, dim3(256), 0, st, p);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+uint32_t kv_padded_len(uint32_t M) { return (M + kBKV - 1) / kBKV * kBKV; }
+
+hipError_t launch_kv_prep(const void* K, const void* V, bool from_q8, _Float16* Kf, _Float16* Vtf, uint32_t Hkv,
+                          uint32_t M, uint32_t D, hipStream_t st) {
+    const uint32_t Mp = kv_padded_len(M);
+    dim3 grid(Mp / kBKV, Hkv);
+    switch (D * 2 + (from_q8 ? 1 : 0)) {
+        case 128: hipLaunchKernelGGL((kv_prep_kernel<64, false>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
+        case 129: hipLaunchKernelGGL((kv_prep_kernel<64, true>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
+        case 256: hipLaunchKernelGGL((kv_prep_kernel<128, false>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
+        case 257: hipLaunchKernelGGL((kv_prep_kernel<128, true>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

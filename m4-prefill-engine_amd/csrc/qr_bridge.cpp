@@ -35,9 +35,12 @@ struct Staged {
 std::vector<Staged> g_staged;      // freed at synchronize
 size_t g_staged_bytes = 0;
 
-// Grow-only scratch for the layer composition.
+// Grow-only scratch for the layer composition, and for the dequantized fp16
+// K / V^T cache of the standalone attention entry points.
 void* g_ws = nullptr;
 size_t g_ws_bytes = 0;
+void* g_attn_ws = nullptr;
+size_t g_attn_ws_bytes = 0;
 
 void set_error(const char* where, hipError_t e) {
     char buf[256];
@@ -365,10 +368,31 @@ int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t 
     void* dv = resolve(Vq, nk / 32 * 34, 4, true, false);
     void* dout = resolve(O, n * 2, 8, false, true);
     if (!dq || !dk || !dv || !dout) return -5;
+    // Q8_0 -> dequantized fp16 K [Hkv, Mp, D] and V^T [Hkv, D, Mp] once, so the
+    // attention kernel stages tiles without decoding them per query tile
+    const uint32_t Mp = qr::kv_padded_len(M);
+    const size_t half_bytes = (size_t)Hkv * Mp * D * 2;
+    if (2 * half_bytes > g_attn_ws_bytes) {
+        if (g_attn_ws) {
+            (void)hipStreamSynchronize(g_stream);
+            (void)hipFree(g_attn_ws);
+            g_attn_ws = nullptr;
+            g_attn_ws_bytes = 0;
+        }
+        hipError_t ea = hipMalloc(&g_attn_ws, 2 * half_bytes);
+        if (ea != hipSuccess) {
+            set_error("hipMalloc(attention cache)", ea);
+            return -5;
+        }
+        g_attn_ws_bytes = 2 * half_bytes;
+    }
+    _Float16* kf = static_cast<_Float16*>(g_attn_ws);
+    _Float16* vtf = kf + half_bytes / 2;
+    hipError_t e = qr::launch_kv_prep(dk, dv, true, kf, vtf, Hkv, M, D, g_stream);
     qr::AttnParams p{static_cast<const _Float16*>(dq), static_cast<const uint8_t*>(dk),
                      static_cast<const uint8_t*>(dv), static_cast<_Float16*>(dout), H, M, D, scale,
-                     o_token_major ? 1 : 0, Hkv};
-    hipError_t e = qr::launch_flash_attn_q8_0(p, g_stream);
+                     o_token_major ? 1 : 0, Hkv, kf, vtf, Mp};
+    if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(p, g_stream);
     finish_outputs();
     if (e != hipSuccess) {
         set_error("flash_attn_q8_0", e);
@@ -441,10 +465,11 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
     }
     std::lock_guard<std::mutex> lk(g_mu);
     const size_t nq = (size_t)M * HQ, nk = (size_t)M * HK;
-    const size_t q8 = nk / 32 * 34;
+    const uint32_t Mp = qr::kv_padded_len(M);
+    const size_t kvf = (size_t)Hkv * Mp * D * 2;  // one dequantized fp16 cache (K or V^T)
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     const bool norms = w_attn || w_ffn;
-    const size_t need = 2 * al(nq * 2) + 2 * al(nk * 2) + 2 * al(q8) + al((size_t)M * dm * 2) +
+    const size_t need = 2 * al(nq * 2) + 2 * al(nk * 2) + 2 * al(kvf) + al((size_t)M * dm * 2) +
                         al((size_t)M * Nm * 2) + (norms ? al((size_t)M * dm * 2) : 0);
     if (need > g_ws_bytes) {
         if (g_ws) {
@@ -465,8 +490,8 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
     _Float16* q = reinterpret_cast<_Float16*>(take(nq * 2));
     _Float16* k = reinterpret_cast<_Float16*>(take(nk * 2));
     _Float16* v = reinterpret_cast<_Float16*>(take(nk * 2));
-    uint8_t* kq = take(q8);
-    uint8_t* vq = take(q8);
+    _Float16* kf = reinterpret_cast<_Float16*>(take(kvf));
+    _Float16* vtf = reinterpret_cast<_Float16*>(take(kvf));
     _Float16* o = reinterpret_cast<_Float16*>(take(nq * 2));
     _Float16* xm = reinterpret_cast<_Float16*>(take((size_t)M * dm * 2));
     _Float16* s = reinterpret_cast<_Float16*>(take((size_t)M * Nm * 2));
@@ -506,9 +531,10 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
         rc = rc ? rc : check(qr::launch_rope(k, Hkv, M, D, theta, offset, traditional, g_stream), "layer rope");
     }
     if (!rc) {
-        hipError_t e = qr::launch_quantize_q8_0(k, kq, nk / 32, g_stream);
-        if (e == hipSuccess) e = qr::launch_quantize_q8_0(v, vq, nk / 32, g_stream);
-        qr::AttnParams ap{q, kq, vq, o, Hq, M, D, scale, 1, Hkv};
+        // Q8_0 KV cache (unified_prefill_engine.mm:554-572) as its dequantized
+        // values: quantize + dequantize in registers, fp16 K and V^T out
+        hipError_t e = qr::launch_kv_prep(k, v, false, kf, vtf, Hkv, M, D, g_stream);
+        qr::AttnParams ap{q, nullptr, nullptr, o, Hq, M, D, scale, 1, Hkv, kf, vtf, Mp};
         if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(ap, g_stream);
         rc = check(e, "layer attention");
     }
@@ -578,7 +604,8 @@ double m4_bridge_get_uma_footprint_mb(void) {
         fclose(f);
     }
     double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
-    return host_mb + (double)(g_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 + g_sk_cnt_n * 4) / (1024.0 * 1024.0);
+    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 + g_sk_cnt_n * 4) /
+                         (1024.0 * 1024.0);
 }
 
 bool m4_bridge_is_initialized(void) {
@@ -593,6 +620,9 @@ void m4_bridge_shutdown(void) {
     if (g_ws) (void)hipFree(g_ws);
     g_ws = nullptr;
     g_ws_bytes = 0;
+    if (g_attn_ws) (void)hipFree(g_attn_ws);
+    g_attn_ws = nullptr;
+    g_attn_ws_bytes = 0;
     if (g_sk_ws) (void)hipFree(g_sk_ws);
     if (g_sk_cnt) (void)hipFree(g_sk_cnt);
     g_sk_ws = nullptr;

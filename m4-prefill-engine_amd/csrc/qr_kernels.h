@@ -52,8 +52,19 @@ struct AttnParams {
     float scale;
     int o_token_major;
     uint32_t Hkv;         // KV heads (grouped-query: query head h reads KV head h / (H / Hkv)); 0 = H
+    // Dequantized fp16 cache (launch_kv_prep) in place of Kq / Vq when Kf is
+    // set: Kf [Hkv, Mp, D], Vtf [Hkv, D, Mp], Mp = kv_padded_len(M).
+    const _Float16* Kf;
+    const _Float16* Vtf;
+    uint32_t Mp;
 };
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st);
+uint32_t kv_padded_len(uint32_t M);
+// K / V ([Hkv, M, D] Q8_0 blocks when from_q8, else fp16) -> the dequantized
+// fp16 cache of the attention kernel (Q8_0 values half(q * half(d)), computed
+// from fp16 inputs by quantizing and dequantizing in registers).
+hipError_t launch_kv_prep(const void* K, const void* V, bool from_q8, _Float16* Kf, _Float16* Vtf, uint32_t Hkv,
+                          uint32_t M, uint32_t D, hipStream_t st);
 
 // RMSNorm over rows of X [M, D] (D % 8 == 0): y = fp16(fp16(x r) w), r =
 // 1 / sqrt(mean(x^2) + eps); norm_type 2 uses fp16(1 + w) in place of w.
