@@ -250,57 +250,73 @@ __device__ __forceinline__ void attn_stage_f16(const AttnRawF16<D>& raw, int tid
 // reference's dequantizer, brick4_attn_bench.mm:57-65); otherwise from fp16
 // K / V through the same quantize-then-dequantize arithmetic as
 // quantize_q8_0_kernel + the Q8_0 path (bit-identical values, no Q8_0 buffer
-// written).  K' rows go straight out; V' is transposed through LDS so V'^T
-// rows leave as 128-byte runs.  Keys M .. Mp - 1 are zero.
+// written).  K units (one key's block) write K' rows straight out; V units
+// (a key pair's blocks) write {V[k][d], V[k+1][d]} words into an LDS tile
+// [d][key], whose rows then leave as 128-byte runs of V'^T.  Keys M .. Mp - 1
+// are zero.
+template <bool FROM_Q8>
+__device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t w[16]) {
+    uint32_t d16, codes[8];  // code word c: codes of elements 4c .. 4c + 3
+    if constexpr (FROM_Q8) {
+        const size_t o = blk * 34;  // 2-byte aligned: nine aligned dwords cover the block
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(src) + (o & ~(size_t)3));
+        uint32_t raw[9];
+#pragma unroll
+        for (int i = 0; i < 9; i++) raw[i] = q[i];
+        const bool par = (o & 2u) != 0;
+        d16 = par ? (raw[0] >> 16) : (raw[0] & 0xffffu);
+#pragma unroll
+        for (int c = 0; c < 8; c++) codes[c] = par ? raw[c + 1] : __builtin_amdgcn_alignbyte(raw[c + 1], raw[c], 2);
+    } else {
+        float x[32];
+        load_block_f16(static_cast<const _Float16*>(src) + blk * 32, x);
+        uint32_t c16[16];
+        quantize_block_q8_0(x, d16, c16);
+#pragma unroll
+        for (int c = 0; c < 8; c++) codes[c] = c16[2 * c] | (c16[2 * c + 1] << 16);
+    }
+    const h2_t d = as_h2(d16 | (d16 << 16));
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        w[2 * c] = q8_pair<false>(codes[c], d);
+        w[2 * c + 1] = q8_pair<true>(codes[c], d);
+    }
+}
+
 template <int D, bool FROM_Q8>
 __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const void* Vsrc, _Float16* Kf, _Float16* Vtf,
                                                       uint32_t M, uint32_t Mp) {
     constexpr int NB = D / 32;            // blocks per key
     constexpr int TR = kBKV + 8;          // LDS row (halfs) of the transposed tile
+    constexpr int KU = kBKV * NB, VU = (kBKV / 2) * NB;
     __shared__ __attribute__((aligned(16))) _Float16 T[D * TR];
     const int tid = threadIdx.x;
     const uint32_t k0 = blockIdx.x * kBKV, hk = blockIdx.y;
-    const size_t head_src = (size_t)M * D, head_dst = (size_t)Mp * D;
-    for (int u = tid; u < 2 * kBKV * NB; u += 256) {
-        const bool isv = u >= kBKV * NB;
-        const int uu = isv ? u - kBKV * NB : u;
-        const int key = uu % kBKV, db = uu / kBKV;
-        const uint32_t gk = k0 + key;
-        uint32_t w[16];  // 32 dequantized halfs
-        if (gk < M) {
-            const size_t blk = hk * (head_src / 32) + (size_t)gk * NB + db;
-            uint32_t d16, codes[16];
-            if constexpr (FROM_Q8) {
-                const uint8_t* b = static_cast<const uint8_t*>(isv ? Vsrc : Ksrc) + blk * 34;
-                const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b);  // 2-byte aligned
-                d16 = b16[0];
-#pragma unroll
-                for (int i = 0; i < 16; i++) codes[i] = b16[1 + i];
-            } else {
-                float x[32];
-                load_block_f16(static_cast<const _Float16*>(isv ? Vsrc : Ksrc) + blk * 32, x);
-                quantize_block_q8_0(x, d16, codes);
-            }
-            const h2_t d = as_h2(d16 | (d16 << 16));
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint32_t q = codes[2 * i] | (codes[2 * i + 1] << 16);
-                w[2 * i] = q8_pair<false>(q, d);
-                w[2 * i + 1] = q8_pair<true>(q, d);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) w[i] = 0u;
-        }
-        if (!isv) {
+    const size_t head_blocks = (size_t)M * NB, head_dst = (size_t)Mp * D;
+    for (int u = tid; u < KU + VU; u += 256) {
+        if (u < KU) {
+            const int key = u % kBKV, db = u / kBKV;
+            const uint32_t gk = k0 + key;
+            uint32_t w[16] = {};
+            if (gk < M) prep_block<FROM_Q8>(Ksrc, hk * head_blocks + (size_t)gk * NB + db, w);
             u4_t* dst = reinterpret_cast<u4_t*>(Kf + hk * head_dst + (size_t)gk * D + db * 32);
 #pragma unroll
             for (int c = 0; c < 4; c++) dst[c] = u4_t{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
         } else {
+            const int v = u - KU;
+            const int kp = v % (kBKV / 2), db = v / (kBKV / 2);
+            uint32_t w[2][16] = {};
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t gk = k0 + 2 * kp + e;
+                if (gk < M) prep_block<FROM_Q8>(Vsrc, hk * head_blocks + (size_t)gk * NB + db, w[e]);
+            }
+            uint32_t* t32 = reinterpret_cast<uint32_t*>(T);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                T[(db * 32 + 2 * i) * TR + key] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
-                T[(db * 32 + 2 * i + 1) * TR + key] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+                const int dd = db * 32 + 2 * i;
+                t32[(dd * TR) / 2 + kp] = perm(w[1][i], w[0][i], 0x05040100u);
+                t32[((dd + 1) * TR) / 2 + kp] = perm(w[1][i], w[0][i], 0x07060302u);
             }
         }
     }
@@ -409,10 +425,16 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 #pragma unroll
         for (int kk = 0; kk < D / 16; kk++) qf[kk] = -qf[kk];
     }
-    float m_run = -INFINITY, l_run = 0.0f;
-    f16v_t o[DT];
+    float m_run = -INFINITY;
+    // o[DT] row 0 accumulates the softmax denominator: the P.V MFMAs also
+    // multiply P by a constant A operand whose row 0 is all ones (lanes of
+    // row j = 0), so the row sums ride on the matrix pipe instead of VALU adds
+    // and use the same fp16 P as the numerator.
+    f16v_t o[DT + 1];
 #pragma unroll
-    for (int t = 0; t < DT; t++) o[t] = f16v_t{};
+    for (int t = 0; t <= DT; t++) o[t] = f16v_t{};
+    const _Float16 one = j == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+    const h8_t ones = {one, one, one, one, one, one, one, one};
 
     auto compute = [&](int kt) {
         const int k0 = kt * kBKV;
@@ -467,23 +489,22 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
         const float m_new = fmaxf(m_run, tmax * c);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
         m_run = m_new;
-        float lsum = 0.0f;
-        uint32_t pk[2][8];  // P as half2 words in accumulator order
+        uint32_t pk[2][8];  // P as half2 words in accumulator order (one RNE pair conversion)
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][r], c, -m_new));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][r + 1], c, -m_new));
-                lsum += e0 + e1;
-                pk[ks][r >> 1] = pack_h2(f2h_bits(e0), f2h_bits(e1));
+                const f2_t e = {e0, e1};
+                pk[ks][r >> 1] = as_u32(__builtin_convertvector(e, h2_t));
             }
-        l_run = l_run * alpha + lsum;
         if (__any(alpha != 1.0f)) {
 #pragma unroll
             for (int t = 0; t < DT; t++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+            o[DT][0] *= alpha;  // the only nonzero row of the denominator tile
         }
 
         // ---- O^T += V^T . P^T : 4 k16 steps over the 64 keys ----
@@ -499,6 +520,7 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
                 for (int t = 0; t < DT; t++)
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[ks][t2][t]), b, o[t], 0,
                                                                   0, 0);
+                o[DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, b, o[DT], 0, 0, 0);
             }
     };
 
@@ -517,7 +539,8 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
     }
 
     // ---- normalize and store ----
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    // denominator of query j: row 0 of the ones tile, held by lane j (lanes 32..63 hold rows 4..7)
+    const float l_tot = __shfl(o[DT][0], j, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < M) {
 #pragma unroll
