@@ -486,9 +486,17 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 #pragma unroll
             for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s[ks][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax * c);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
-        m_run = m_new;
+        // Lazy running maximum: the reference point moves only when some lane's
+        // tile maximum exceeds it by more than 2^8 (P <= 256 in the meantime,
+        // well inside fp16 and fp32); the output rescale is skipped otherwise.
+        const float m_cand = tmax * c;
+        float alpha = 1.0f;
+        if (__any(m_cand > m_run + 8.0f)) {  // always taken on the first tile (m_run = -inf)
+            const float m_new = fmaxf(m_run, m_cand);
+            alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
+            m_run = m_new;
+        }
+        const float m_new = m_run;
         uint32_t pk[2][8];  // P as half2 words in accumulator order (one RNE pair conversion)
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
