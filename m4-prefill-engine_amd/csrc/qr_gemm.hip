@@ -479,7 +479,7 @@ static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
     if constexpr (DUAL) {
         return rb_launch_cfg<F, 4, 1, 4, true>(p, st);
     } else {
-        switch (rb_pick(F, p.M, false)) {
+        switch (rb_pick(F, p.M, p.N, false)) {
             case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);
             case 3: return rb_launch_cfg<F, QR_RB_BIG_K, false>(p, st);
             default: return rb_launch_cfg<F, QR_RB_MID, false>(p, st);

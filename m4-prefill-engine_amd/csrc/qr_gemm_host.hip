@@ -21,7 +21,7 @@ hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
 }
 
 uint32_t gemm_pick_ksplit(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.W2 != nullptr));
     const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
     // One workgroup fits a CU (its registers), so the grid runs in waves of
     // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
@@ -33,14 +33,14 @@ uint32_t gemm_pick_ksplit(const GemmParams& p) {
 
 size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
     const bool dual = p.W2 != nullptr;
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, dual));
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, dual));
     const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
     if (tiles) *tiles = T;
     return ks > 1 ? (size_t)ks * T * d.bm * d.bn * (dual ? 2 : 1) : 0;
 }
 
 uint32_t gemm_group_m(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.W2 != nullptr));
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.W2 != nullptr));
     const uint32_t nt_m = (p.M + d.bm - 1) / d.bm;
     return nt_m >= 4 ? 4u : 2u;
 }

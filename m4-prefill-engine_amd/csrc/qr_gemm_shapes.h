@@ -28,9 +28,21 @@ template <int TM, int TN, int NW> struct ShapeOf {
 struct RbShape {
     uint32_t bm, bn;
 };
-inline int rb_pick(int format, uint32_t M, bool dual) {
+#ifndef QR_RB_MID_FILL
+#define QR_RB_MID_FILL 1
+#endif
+// Shape choice.  At M >= 1024 the wide tile is used while it alone fills the
+// 256 CUs; when it cannot (N small), 128 x 128 tiles give twice the tiles, so
+// the K split -- whose fp32 partials are M x N x 4 bytes written and read per
+// extra split -- is halved or avoided.
+inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     if (dual) return 2;
-    if (M >= 1024) return format == QUANT_Q4_K ? 3 : 0;
+    if (M >= 1024) {
+        if (format == QUANT_Q4_K) return 3;
+        const uint32_t big_tiles = ((M + 127) / 128) * ((N + 255) / 256);
+        if (QR_RB_MID_FILL && big_tiles < 256) return 1;
+        return 0;
+    }
     return 1;
 }
 inline RbShape rb_dims(int s) {
