@@ -210,7 +210,7 @@ gemm_rb_kernel(GemmParams p) {
     // ops alternate, so the decode issues while the matrix pipe is busy.
     constexpr int NM = TM * NCB;            // MFMAs per slice
     constexpr int HALVES = 2 * NCB;         // half-group decodes per step
-    static_assert(HALVES <= 4, "at most one half decode per slice");
+    constexpr int DPS = (HALVES + 3) / 4;   // half-group decodes per slice
     auto step_body = [&](uint32_t s, int j) {
         const int wslot = (j + 1) % WP;
         uint32_t (*bn)[16] = bw[(j + 1) & 1];
@@ -228,8 +228,9 @@ gemm_rb_kernel(GemmParams p) {
                 for (int i = 0; i < TM; i++)
                     acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk & 1][i], b, acc[i][jb], 0, 0, 0);
             }
-            if (kk < HALVES) {
-                const int jb = kk >> 1, hh = kk & 1;
+#pragma unroll
+            for (int d = kk * DPS; d < (kk + 1) * DPS && d < HALVES; d++) {
+                const int jb = d >> 1, hh = d & 1;
                 const uint32_t par = Dec::parity((uint32_t)bcol(jb) * col_bytes, gn);
                 decode_half_fast<F>(wraw[wslot][jb], par, hh, bn[jb] + 8 * hh);
             }
@@ -477,7 +478,7 @@ static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
 template <int F, bool DUAL>
 static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
     if constexpr (DUAL) {
-        return rb_launch_cfg<F, 4, 1, 4, true>(p, st);
+        return rb_launch_cfg<F, QR_RB_DUAL, true>(p, st);
     } else {
         switch (rb_pick(F, p.M, p.N, false)) {
             case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);

@@ -22,6 +22,9 @@ namespace qr {
 #ifndef QR_RB_MID
 #define QR_RB_MID 4, 1, 4
 #endif
+#ifndef QR_RB_DUAL
+#define QR_RB_DUAL 4, 1, 4
+#endif
 template <int TM, int TN, int NW> struct ShapeOf {
     static constexpr uint32_t bm = 32 * TM, bn = 32 * TN * NW;
 };
@@ -50,7 +53,7 @@ inline RbShape rb_dims(int s) {
         case 0: return {ShapeOf<QR_RB_BIG>::bm, ShapeOf<QR_RB_BIG>::bn};
         case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
         case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
-        default: return {128, 128};
+        default: return {ShapeOf<QR_RB_DUAL>::bm, ShapeOf<QR_RB_DUAL>::bn};
     }
 }
 

@@ -590,3 +590,17 @@ def test_prefill_layer_ex(bridge, oracle, norm_type, rope, traditional, Hkv):
     # fp16 intermediates on both sides; a tie flipped upstream (norm, RoPE) moves
     # a downstream value by about one output step
     assert d <= 2 * TOL
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("M,K,N", [(1030, 1024, 200), (2048, 2048, 512), (1024, 4096, 264)])
+def test_tall_narrow_projections(bridge, oracle, fmt, M, K, N):
+    """M >= 1024 with N too small for the wide tile to fill the GPU: the
+    128 x 128 tile with (or without) a K split; ragged M and N edges."""
+    X = synth.activations(M, K, 95 + fmt)
+    W = synth.quantized_weights(fmt, N, K, 96 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    ref = oracle.gemm(fmt, X, W, N)
+    assert maxdiff(host(Y), ref) <= TOL
