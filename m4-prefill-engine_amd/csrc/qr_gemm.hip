@@ -88,8 +88,15 @@ __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt
 
 }  // namespace rb
 
-template <int F, int TM, int TN, int NW, bool DUAL, int P>
-__global__ void __launch_bounds__(64 * NW)
+#ifndef QR_RB_DUAL_OCC
+#define QR_RB_DUAL_OCC 1
+#endif
+// SPLIT: the instance carries the split-K reduction (its second accumulator
+// set and batched partial loads need registers); the SwiGLU instance without
+// it is sized for QR_RB_DUAL_OCC workgroups per CU, so one workgroup's
+// prologue and epilogue overlap another's main loop.
+template <int F, int TM, int TN, int NW, bool DUAL, int P, bool SPLIT>
+__global__ void __launch_bounds__(64 * NW, ((DUAL && !SPLIT) ? QR_RB_DUAL_OCC : 1))
 gemm_rb_kernel(GemmParams p) {
     using C = rb::Cfg<TM, TN, NW, DUAL>;
     using Dec = Decoder<F>;
@@ -292,7 +299,7 @@ gemm_rb_kernel(GemmParams p) {
     // whose L2s are not coherent with each other: they are written and read
     // with 64-bit agent-scope atomics (write-through / read-from-memory); the
     // reads are issued in batches of up to 32 so their latencies overlap.
-    if (ksplit > 1) {
+    if (SPLIT && ksplit > 1) {
         constexpr int NP = C::ACC / 2;                 // float pairs per thread
         constexpr int BATCH = NP < 32 ? NP : 32;       // pairs in flight per batch
         static_assert(NP % BATCH == 0 && BATCH % 8 == 0, "whole 32x32 tiles per batch");
@@ -467,7 +474,8 @@ gemm_rb_kernel(GemmParams p) {
 template <int F, int TM, int TN, int NW, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     using C = rb::Cfg<TM, TN, NW, DUAL>;
-    auto kern = gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES>;
+    auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES, true>
+                             : gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES, false>;
     const size_t lds = C::LDS_BYTES;
     const uint32_t T = ((p.M + C::BM - 1) / C::BM) * ((p.N + C::BN - 1) / C::BN);
     const uint32_t ks = p.ksplit ? p.ksplit : 1;
