@@ -138,6 +138,14 @@ def test_uninitialized_bridge_refuses_work(lib):
                                        0, 128, 64) == -1
     assert lib.m4_bridge_dispatch_router_gemm(x.ctypes.data, x.nbytes, w.ctypes.data, w.nbytes, y.ctypes.data,
                                               y.nbytes, 7, 64, 128, 64) == -1
+    assert lib.m4_bridge_rmsnorm(x.ctypes.data, x.nbytes, w.ctypes.data, 256, x.ctypes.data, x.nbytes, 64, 128,
+                                 1e-5, 1) == -1
+    assert lib.m4_bridge_rope(x.ctypes.data, x.nbytes, 1, 64, 128, 1e4, 0, 0) == -1
+    assert lib.m4_bridge_dispatch_flash_attn_q8_0_gqa(x.ctypes.data, x.nbytes, w.ctypes.data, w.nbytes,
+                                                      w.ctypes.data, w.nbytes, y.ctypes.data, y.nbytes,
+                                                      2, 1, 32, 64, 0.125, 0) == -1
+    assert lib.m4_bridge_prefill_layer_ex(*([x.ctypes.data] * 11), 0, 64, 128, 2, 1, 64, 256, 0.125, 1, 1e-5, 1,
+                                          1e4, 0, 0) == -1
     lib.m4_bridge_synchronize()
     lib.m4_bridge_shutdown()
     assert lib.m4_bridge_get_uma_footprint_mb() > 0.0
@@ -151,3 +159,21 @@ def test_python_bridge_maps_status_to_runtime_error(libpath):
     b = m4_bridge.HIPBridge(libpath)
     with pytest.raises(RuntimeError, match="status code -1"):
         b.dispatch_gemm(np.zeros((4, 32), np.float16), np.zeros(18 * 4, np.uint8), np.zeros((4, 4), np.float16), 0)
+
+
+def test_non_finite_tripwire_host_side():
+    """tests/e2e/test_tier1_feature_coverage.mm:490-531: a clean buffer passes;
+    a NaN or Inf anywhere (fp32 or fp16, numpy or torch) trips the check the
+    bridge defers to synchronize."""
+    import torch
+
+    clean = np.full(1000, 1.234, np.float32)
+    assert m4_bridge._all_finite(clean)
+    for bad in (np.nan, np.inf):
+        a = np.ones(1000, np.float32)
+        a[42] = bad
+        assert not m4_bridge._all_finite(a)
+        h = np.full(100, 0.5, np.float16)
+        h[77] = bad
+        assert not m4_bridge._all_finite(h) and not m4_bridge._all_finite(h.view(np.uint16))
+        assert not m4_bridge._all_finite(torch.from_numpy(h))

@@ -604,3 +604,57 @@ def test_tall_narrow_projections(bridge, oracle, fmt, M, K, N):
     bridge.synchronize()
     ref = oracle.gemm(fmt, X, W, N)
     assert maxdiff(host(Y), ref) <= TOL
+
+
+
+def test_deferred_tripwire_on_device_output(bridge):
+    """A projection whose output is not finite (Q4_0 scales of +inf: (q - 8) inf
+    is inf or NaN) raises FloatingPointError at synchronize when the dispatch
+    asked for the check (core/bridge/m4_bridge.py:176-177, 227-233); the same
+    call without the check, and a clean one with it, do not."""
+    M, K, N = 40, 256, 64
+    W = synth.random_blocks(0, N, K, 5).reshape(N, K // 32, 18).copy()
+    W[..., 0:2] = np.array([np.inf], np.float16).view(np.uint8)
+    W = W.reshape(-1)
+    X = synth.activations(M, K, 6)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, 0, M, K, N, check_finite=True)
+    with pytest.raises(FloatingPointError):
+        bridge.synchronize()
+    bridge.dispatch_gemm(dev(X), dev(W), Y, 0, M, K, N)
+    bridge.synchronize()
+    Wc = synth.random_blocks(0, N, K, 7)
+    bridge.dispatch_gemm(dev(X), dev(Wc), Y, 0, M, K, N, check_finite=True)
+    bridge.synchronize()
+
+
+def test_extension_entry_points_error_codes(bridge):
+    """Argument checks of the block-extra entry points, before any device work."""
+    lib = bridge.lib
+    x = empty16(64, 128)
+    w = empty16(128)
+    assert lib.m4_bridge_rmsnorm(x.data_ptr(), x.numel() * 2, w.data_ptr(), 256, x.data_ptr(), x.numel() * 2, 64,
+                                 128, 1e-5, 3) == -3
+    assert lib.m4_bridge_rmsnorm(x.data_ptr(), x.numel() * 2, w.data_ptr(), 256, x.data_ptr(), x.numel() * 2, 64,
+                                 124, 1e-5, 1) == -4
+    assert lib.m4_bridge_rmsnorm(None, 0, w.data_ptr(), 256, x.data_ptr(), x.numel() * 2, 64, 128, 1e-5, 1) == -2
+    assert lib.m4_bridge_rmsnorm(x.data_ptr(), 100, w.data_ptr(), 256, x.data_ptr(), x.numel() * 2, 64, 128,
+                                 1e-5, 1) == -2
+    assert lib.m4_bridge_rope(x.data_ptr(), x.numel() * 2, 1, 64, 120, 1e4, 0, 0) == -4
+    assert lib.m4_bridge_rope(x.data_ptr(), x.numel() * 2, 1, 64, 128, 0.0, 0, 0) == -4
+    assert lib.m4_bridge_rope(x.data_ptr(), 16, 1, 64, 128, 1e4, 0, 0) == -2
+    q8 = torch_empty_u8(64 * 128 // 32 * 34)
+    assert lib.m4_bridge_dispatch_flash_attn_q8_0_gqa(x.data_ptr(), x.numel() * 2, q8.data_ptr(), q8.numel(),
+                                                      q8.data_ptr(), q8.numel(), x.data_ptr(), x.numel() * 2,
+                                                      2, 3, 64, 64, 0.125, 0) == -4
+    p = [x.data_ptr()] * 11
+    assert lib.m4_bridge_prefill_layer_ex(*p, 0, 64, 128, 4, 3, 64, 256, 0.125, 1, 1e-5, 1, 1e4, 0, 0) == -4
+    assert lib.m4_bridge_prefill_layer_ex(*p, 0, 64, 128, 4, 2, 64, 256, 0.125, 5, 1e-5, 1, 1e4, 0, 0) == -3
+    assert lib.m4_bridge_prefill_layer_ex(*p[:2], None, *p[3:], 0, 64, 128, 4, 2, 64, 256, 0.125, 1, 1e-5, 1, 1e4,
+                                          0, 0) == -2
+
+
+def torch_empty_u8(n):
+    import torch
+
+    return torch.empty(n, dtype=torch.uint8, device="cuda")
