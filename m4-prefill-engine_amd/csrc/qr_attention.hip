@@ -564,10 +564,292 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
     }
 }
 
+// --------------------------------------------------------------------------
+// Balanced causal attention over the fp16 cache (D = 64): one workgroup of 8
+// waves per (light, heavy) query-tile pair of one head -- query tiles a and
+// qtiles - 1 - a -- so every workgroup carries the same number of key tiles
+// and every SIMD keeps two waves busy until the end (with one query tile per
+// workgroup, a CU's light workgroup finishes early and its SIMDs are left
+// with a single wave for most of the kernel).  Wave group 0 takes the light
+// tile's queries over key tiles [0, Tl), group 1 the heavy tile's over [0, Tl);
+// on key tiles [Tl, Th) both groups take the heavy queries, group 0 the first
+// 32 keys of each tile and group 1 the last 32; at the end group 0's partial
+// softmax state for the heavy queries is merged into group 1's through LDS.
+// The per-tile arithmetic is that of flash_attn_q8_0_kernel.
+// --------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
+    constexpr int KROW = D + 8, VROW = kBKV + 8, DT = D / 32;
+    constexpr int NT = 512;
+    constexpr int KCH = kBKV * (D / 8) / NT;   // 16-byte K chunks per thread and tile
+    constexpr int VCH = D * (kBKV / 8) / NT;   // 16-byte V^T chunks per thread and tile
+    static_assert(KCH >= 1 && VCH >= 1, "whole chunks per thread");
+    // one LDS array: K tiles [2][key][d], V^T tiles [2][d][key]; reused by the final merge
+    constexpr int KT = kBKV * KROW, VT = D * VROW;
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * KT + 2 * VT];
+    auto Ks = [&](int buf) { return smem + buf * KT; };
+    auto Vt = [&](int buf) { return smem + 2 * KT + buf * VT; };
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = wave >> 2, wq = wave & 3;
+    const int g = lane >> 5, j = lane & 31;
+    const int M = (int)p.M, Mp = (int)p.Mp;
+    const int qtiles = (M + kBQ - 1) / kBQ;
+    const int pr = (int)blockIdx.x / (int)p.H, h = (int)blockIdx.x % (int)p.H;
+    const int qa = pr, qb = qtiles - 1 - pr;   // light and heavy query tiles (qa <= qb)
+    auto tiles_for = [&](int qt) { return (min((qt + 1) * kBQ, M) - 1) / kBKV + 1; };
+    const int Tl = qa == qb ? 0 : tiles_for(qa);
+    const int Th = tiles_for(qb);
+
+    const size_t head_elems = (size_t)M * D;
+    const int hk = p.Hkv ? h / ((int)p.H / (int)p.Hkv) : h;
+    const uint32_t cbytes = (uint32_t)((size_t)Mp * D * 2);
+    auto kr = make_rsrc(p.Kf + (size_t)hk * Mp * D, cbytes);
+    auto vr = make_rsrc(p.Vtf + (size_t)hk * Mp * D, cbytes);
+    auto qr_ = make_rsrc(p.Q + (size_t)h * head_elems, (uint32_t)(head_elems * 2));
+
+    struct Raw { u4_t k[KCH]; u4_t v[VCH]; };
+    auto fetch = [&](int t, Raw& r) {
+        const int k0 = t * kBKV;
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int c = tid + NT * i;
+            r.k[i] = ld_b128(kr, (uint32_t)((k0 + c / (D / 8)) * D + (c % (D / 8)) * 8) * 2u);
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int c = tid + NT * i;
+            r.v[i] = ld_b128(vr, (uint32_t)((c / 8) * Mp + k0 + (c % 8) * 8) * 2u);
+        }
+    };
+    auto stage = [&](const Raw& r, int buf) {
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int c = tid + NT * i;
+            *reinterpret_cast<u4_t*>(Ks(buf) + (c / (D / 8)) * KROW + (c % (D / 8)) * 8) = r.k[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int c = tid + NT * i;
+            *reinterpret_cast<u4_t*>(Vt(buf) + (c / 8) * VROW + (c % 8) * 8) = r.v[i];
+        }
+    };
+
+    // scale in log2 units; a negative scale flips the sign of Q (exact)
+    float c = p.scale * 1.4426950408889634f;
+    const bool neg = c < 0.0f;
+    if (neg) c = -c;
+
+    // per-wave state: the queries qw .. qw + 31 it currently owns
+    int qw = 0;
+    h8_t qf[D / 16];
+    float m_run = -INFINITY;
+    f16v_t o[DT + 1];
+    const _Float16 one = j == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+    const h8_t ones = {one, one, one, one, one, one, one, one};
+    auto begin = [&](int qt) {  // take the queries of tile qt, fresh state
+        qw = qt * kBQ + wq * 32;
+        const int my_q = qw + j;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; kk++) {
+            const uint32_t off = my_q < M ? ((uint32_t)my_q * D + kk * 16 + 8 * g) * 2u : kOOB;
+            qf[kk] = __builtin_bit_cast(h8_t, ld_b128(qr_, off));
+            if (neg) qf[kk] = -qf[kk];
+        }
+        m_run = -INFINITY;
+#pragma unroll
+        for (int t = 0; t <= DT; t++) o[t] = f16v_t{};
+    };
+    auto store = [&](float inv) {
+        const int my_q = qw + j;
+        if (my_q >= M) return;
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                const int d0 = t * 32 + 8 * r4 + 4 * g;
+                const f2_t a = {o[t][4 * r4] * inv, o[t][4 * r4 + 1] * inv};
+                const f2_t b = {o[t][4 * r4 + 2] * inv, o[t][4 * r4 + 3] * inv};
+                const size_t idx = p.o_token_major ? ((size_t)my_q * p.H + h) * D + d0
+                                                   : (size_t)h * head_elems + (size_t)my_q * D + d0;
+                *reinterpret_cast<u2_t*>(p.O + idx) =
+                    u2_t{as_u32(__builtin_convertvector(a, h2_t)), as_u32(__builtin_convertvector(b, h2_t))};
+            }
+    };
+
+    // one key tile (or its 32-key half ks0) for the wave's current queries
+    auto compute = [&](int kt, int ks0, int nks) {
+        const int k0 = kt * kBKV;
+        if (k0 + 32 * ks0 > qw + 31) return;  // the keys handled lie above this wave's diagonal
+        const int my_q = qw + j;
+        const _Float16* Kb = Ks(kt & 1);
+        const _Float16* Vb = Vt(kt & 1);
+        h8_t ka[2][D / 16];
+        f16v_t s[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e >= nks) break;
+#pragma unroll
+            for (int kk = 0; kk < D / 16; kk++)
+                ka[e][kk] = *reinterpret_cast<const h8_t*>(Kb + ((ks0 + e) * 32 + j) * KROW + kk * 16 + 8 * g);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e >= nks) break;
+            s[e] = f16v_t{};
+#pragma unroll
+            for (int kk = 0; kk < D / 16; kk++)
+                s[e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[e][kk], qf[kk], s[e], 0, 0, 0);
+        }
+        u4_t va[2][2][DT];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e >= nks) break;
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int t = 0; t < DT; t++) {
+                    const _Float16* row = Vb + (t * 32 + j) * VROW + (ks0 + e) * 32 + t2 * 16 + 4 * g;
+                    const u2_t lo = *reinterpret_cast<const u2_t*>(row);
+                    const u2_t hi = *reinterpret_cast<const u2_t*>(row + 8);
+                    va[e][t2][t] = u4_t{lo.x, lo.y, hi.x, hi.y};
+                }
+        }
+        if (k0 + 32 * (ks0 + nks) - 1 > qw) {  // keys crossing the diagonal: causal mask
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                if (e >= nks) break;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = k0 + (ks0 + e) * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    s[e][r] = (key <= my_q && key < M) ? s[e][r] : -INFINITY;
+                }
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e >= nks) break;
+#pragma unroll
+            for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s[e][r]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_cand = tmax * c;
+        float alpha = 1.0f;
+        if (__any(m_cand > m_run + 8.0f)) {  // lazy reference point (P <= 2^8 otherwise)
+            const float m_new = fmaxf(m_run, m_cand);
+            alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+        }
+        uint32_t pk[2][8];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e >= nks) break;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const f2_t ee = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[e][r], c, -m_run)),
+                                 __builtin_amdgcn_exp2f(__builtin_fmaf(s[e][r + 1], c, -m_run))};
+                pk[e][r >> 1] = as_u32(__builtin_convertvector(ee, h2_t));
+            }
+        }
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < DT; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+            o[DT][0] *= alpha;
+        }
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e >= nks) break;
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++) {
+                const h8_t b = __builtin_bit_cast(
+                    h8_t, u4_t{pk[e][4 * t2], pk[e][4 * t2 + 1], pk[e][4 * t2 + 2], pk[e][4 * t2 + 3]});
+#pragma unroll
+                for (int t = 0; t < DT; t++)
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[e][t2][t]), b, o[t], 0,
+                                                                  0, 0);
+                o[DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, b, o[DT], 0, 0, 0);
+            }
+        }
+    };
+    auto step = [&](int t) {
+        if (t < Tl) {
+            compute(t, 0, 2);          // group 0: light queries, group 1: heavy queries
+        } else {
+            compute(t, grp, 1);        // both: heavy queries, one 32-key half each
+        }
+    };
+
+    begin(grp == 0 && Tl > 0 ? qa : qb);
+    Raw rA, rB;
+    fetch(0, rA);
+    if (Th > 1) fetch(1, rB);
+    stage(rA, 0);
+    __syncthreads();
+    for (int t = 0; t < Th; t += 2) {
+        if (t + 2 < Th) fetch(t + 2, rA);
+        step(t);
+        if (grp == 0 && t + 1 == Tl) {  // light tile done: write it, take the heavy queries
+            store(1.0f / __shfl(o[DT][0], j, 64));
+            begin(qb);
+        }
+        if (t + 1 < Th) stage(rB, (t + 1) & 1);
+        __syncthreads();
+        if (t + 1 >= Th) break;
+        if (t + 3 < Th) fetch(t + 3, rB);
+        step(t + 1);
+        if (grp == 0 && t + 2 == Tl) {
+            store(1.0f / __shfl(o[DT][0], j, 64));
+            begin(qb);
+        }
+        if (t + 2 < Th) stage(rA, (t + 2) & 1);
+        __syncthreads();
+    }
+
+    // ---- merge group 0's partial state for the heavy queries into group 1's ----
+    constexpr int SW = DT * 16 + 2;  // floats per lane: o[0..DT-1], row 0 of o[DT], m
+    float* X = reinterpret_cast<float*>(smem);
+    static_assert(4 * 64 * SW * 4 <= (int)sizeof(smem), "merge buffer fits the tile stages");
+    if (grp == 0) {
+        float* x = X + (wq * 64 + lane);
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) x[(t * 16 + r) * 256] = o[t][r];
+        x[(DT * 16) * 256] = o[DT][0];
+        x[(DT * 16 + 1) * 256] = m_run;
+    }
+    __syncthreads();
+    if (grp == 1) {
+        const float* x = X + (wq * 64 + lane);
+        const float ma = x[(DT * 16 + 1) * 256];
+        const float m = fmaxf(ma, m_run);
+        const float fa = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - m);
+        const float fb = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[t][r] = o[t][r] * fb + x[(t * 16 + r) * 256] * fa;
+        o[DT][0] = o[DT][0] * fb + x[(DT * 16) * 256] * fa;
+        const float l = __shfl(o[DT][0], j, 64);
+        store(l > 0.0f ? 1.0f / l : 0.0f);
+    }
+}
+
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
     const bool f16 = p.Kf != nullptr;
     if (f16 && (p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV)) return hipErrorInvalidValue;
+#ifndef QR_ATTN_PAIR
+#define QR_ATTN_PAIR 1
+#endif
+    if (QR_ATTN_PAIR && f16 && p.D == 64) {
+        const uint32_t qtiles = (p.M + kBQ - 1) / kBQ;
+        hipLaunchKernelGGL((flash_attn_pair_kernel<64>), dim3(((qtiles + 1) / 2) * p.H), dim3(512), 0, st, p);
+        return hipGetLastError();
+    }
     switch (p.D) {
         case 64:
             if (f16) hipLaunchKernelGGL((flash_attn_q8_0_kernel<64, true>), grid, dim3(256), 0, st, p);
