@@ -577,6 +577,9 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 // softmax state for the heavy queries is merged into group 1's through LDS.
 // The per-tile arithmetic is that of flash_attn_q8_0_kernel.
 // --------------------------------------------------------------------------
+#ifndef QR_ATTN_PREF
+#define QR_ATTN_PREF 2
+#endif
 template <int D>
 __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     constexpr int KROW = D + 8, VROW = kBKV + 8, DT = D / 32;
@@ -783,29 +786,29 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     };
 
     begin(grp == 0 && Tl > 0 ? qa : qb);
-    Raw rA, rB;
-    fetch(0, rA);
-    if (Th > 1) fetch(1, rB);
-    stage(rA, 0);
+    // raw K / V^T tiles fetched R tiles ahead (a ring of R register sets,
+    // loop unrolled by R so every slot index is static)
+    constexpr int R = QR_ATTN_PREF;
+    Raw raw[R];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (r < Th) fetch(r, raw[r]);
+    stage(raw[0], 0);
     __syncthreads();
-    for (int t = 0; t < Th; t += 2) {
-        if (t + 2 < Th) fetch(t + 2, rA);
-        step(t);
-        if (grp == 0 && t + 1 == Tl) {  // light tile done: write it, take the heavy queries
-            store(1.0f / __shfl(o[DT][0], j, 64));
-            begin(qb);
+    for (int t0 = 0; t0 < Th; t0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int t = t0 + r;
+            if (t >= Th) break;
+            if (t + R < Th) fetch(t + R, raw[r]);
+            step(t);
+            if (grp == 0 && t + 1 == Tl) {  // light tile done: write it, take the heavy queries
+                store(1.0f / __shfl(o[DT][0], j, 64));
+                begin(qb);
+            }
+            if (t + 1 < Th) stage(raw[(r + 1) % R], (t + 1) & 1);
+            __syncthreads();
         }
-        if (t + 1 < Th) stage(rB, (t + 1) & 1);
-        __syncthreads();
-        if (t + 1 >= Th) break;
-        if (t + 3 < Th) fetch(t + 3, rB);
-        step(t + 1);
-        if (grp == 0 && t + 2 == Tl) {
-            store(1.0f / __shfl(o[DT][0], j, 64));
-            begin(qb);
-        }
-        if (t + 2 < Th) stage(rA, (t + 2) & 1);
-        __syncthreads();
     }
 
     // ---- merge group 0's partial state for the heavy queries into group 1's ----
