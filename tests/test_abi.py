@@ -177,3 +177,23 @@ def test_non_finite_tripwire_host_side():
         h[77] = bad
         assert not m4_bridge._all_finite(h) and not m4_bridge._all_finite(h.view(np.uint16))
         assert not m4_bridge._all_finite(torch.from_numpy(h))
+
+
+def test_c_caller_compiles_and_links(libpath, tmp_path):
+    """The headers are plain C and the library links from a C program: build
+    tests/c/abi_smoke.c with the host compiler against the shipped .so and run
+    it (entry points that need no GPU)."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    exe = tmp_path / "abi_smoke"
+    r = subprocess.run([cc, "-std=c99", "-Wall", "-Werror", "-I", str(ROOT / "include"), str(ROOT / "tests" / "c" /
+                        "abi_smoke.c"), "-o", str(exe), "-L", str(libpath.parent), "-lm4_bridge",
+                        f"-Wl,-rpath,{libpath.parent}"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "abi_smoke: ok" in r.stdout
