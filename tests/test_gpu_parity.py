@@ -303,7 +303,7 @@ def test_direct_head_and_residual(bridge, oracle, fmt):
 # SwiGLU
 # --------------------------------------------------------------------------
 
-@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("M", [33, 128, 129])
 def test_swiglu(bridge, oracle, fmt, M):
     # brick3_swiglu_bench.mm:268-426 verifies M in {33,127,128,129}
