@@ -4,22 +4,19 @@
 // Replaces quantize_kv_to_q8_0 (unified_kernels.metal:118-145) and
 // flash_attn_mma_64x64_q8_0_impl<D> (brick4_attn_kernels.metal:572-881).
 //
-// Attention design (one workgroup = 4 wave64s = 128 queries of one head):
+//  * The Q8_0 cache is dequantized once per call into an fp16 cache (K' rows,
+//    V' transposed), each value the reference's half(q * half(d))
+//    (brick4_attn_bench.mm:57-65), so query tiles stage K/V tiles with plain
+//    copies instead of decoding them again per query tile.
 //  * Each wave owns 32 queries and computes S^T = K . Q^T with
 //    v_mfma_f32_32x32x16_f16, so a lane owns ONE query column: the softmax
 //    row statistics are lane-local over its 16 accumulator rows plus one
 //    exchange with the partner lane (l ^ 32) -- no 32-lane reduction trees.
-//  * K/V tiles of 64 keys are dequantized once per workgroup from Q8_0 into
-//    LDS (K as [key][d], V transposed as [d][key]); the binary16 value is the
-//    exact product q * d rounded once, as the reference's dequantizer
-//    (brick4_attn_bench.mm:57-65).
 //  * P stays in registers: the S^T accumulator of a lane already holds the
 //    8 keys that lane must supply as the B operand of O^T = V^T . P^T, given
 //    the matching key order in the V^T A-operand reads (two ds_read_b64).
 //  * fp32 running max / sum / output accumulators (the reference keeps
 //    S, P and O in half); the output is rounded to fp16 once.
-#include <type_traits>
-
 #include "qr_device.h"
 #include "qr_kernels.h"
 
@@ -98,117 +95,6 @@ __device__ __forceinline__ uint32_t q8_pair(uint32_t codes, h2_t d) {
     const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
     const uint32_t u = codes ^ 0x80808080u;  // two's complement byte -> q + 128
     return as_u32((as_h2(HI ? nib_pair_hi(u) : nib_pair_lo(u)) - off) * d);
-}
-
-// Tile staging.  Per 64-key tile, one "unit" per thread and pass:
-//  K unit  = one Q8_0 block (key, 32 dims) -> 32 halfs of row `key` of Ks;
-//  V unit  = 16 dims of two adjacent keys  -> 16 half2 {V[k][d], V[k+1][d]}
-//            written to rows d of the transposed tile Vt[d][key].
-// Raw words are fetched one tile ahead of the decode (two register sets).
-template <int D>
-struct AttnStage {
-    static constexpr int NB = D / 32;                 // Q8_0 blocks per key
-    static constexpr int KU = kBKV * NB;              // K units per tile
-    static constexpr int VU = (kBKV / 2) * (D / 16);  // V units per tile
-    static constexpr int UPT = (KU + VU) / 256;       // units per thread
-    static_assert((KU + VU) % 256 == 0 && KU % 64 == 0, "whole passes; each wave stages only K or only V");
-};
-
-// Raw words of one thread's units: K units use k (9 words: the block's dwords),
-// V units v (two keys x {scale dword, 5 code dwords}).  Separate arrays, so the
-// two unit kinds never share a register slot.
-template <int D>
-struct AttnRaw {
-    uint32_t k[AttnStage<D>::UPT][9];
-    uint32_t v[AttnStage<D>::UPT][12];
-};
-
-template <int D>
-__device__ __forceinline__ void attn_fetch(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int k0, int M, int tid,
-                                           AttnRaw<D>& raw) {
-    using S = AttnStage<D>;
-#pragma unroll
-    for (int i = 0; i < S::UPT; i++) {
-        const int u = tid + 256 * i;
-        if (__builtin_amdgcn_readfirstlane(u) < S::KU) {  // wave-uniform: K units fill whole waves
-            const int key = u % kBKV, db = u / kBKV;
-            const int gk = k0 + key;
-            const uint32_t o = gk < M ? (uint32_t)(gk * S::NB + db) * 34u : kOOB;
-            const uint32_t a = o & ~3u;
-#pragma unroll
-            for (int w = 0; w < 9; w++) raw.k[i][w] = ld_b32(kr, a + 4u * w);
-            asm volatile("; staged K fetch" ::: "memory");  // keeps the branches' stores apart (SROA)
-        } else {
-            const int v = u - S::KU;
-            const int kp = v % (kBKV / 2), dg = v / (kBKV / 2);  // key pair, 16-dim group
-            const int db = dg >> 1, hh = dg & 1;
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int gk = k0 + 2 * kp + e;
-                const uint32_t o = gk < M ? (uint32_t)(gk * S::NB + db) * 34u : kOOB;
-                const uint32_t cs = o + 2u + 16u * (uint32_t)hh;  // first code byte
-                const uint32_t a = cs & ~3u;
-                raw.v[i][6 * e] = ld_b32(vr, o & ~3u);             // holds d
-#pragma unroll
-                for (int w = 0; w < 5; w++) raw.v[i][6 * e + 1 + w] = ld_b32(vr, a + 4u * w);
-            }
-            asm volatile("; staged V fetch" ::: "memory");
-        }
-    }
-}
-
-template <int D>
-__device__ __forceinline__ void attn_stage(const AttnRaw<D>& raw, int k0, int tid,
-                                           _Float16* Ks, _Float16* Vt) {
-    using S = AttnStage<D>;
-    constexpr int KROW = D + 8, VROW = kBKV + 8;
-#pragma unroll
-    for (int i = 0; i < S::UPT; i++) {
-        const int u = tid + 256 * i;
-        if (__builtin_amdgcn_readfirstlane(u) < S::KU) {
-            const int key = u % kBKV, db = u / kBKV;
-            const uint32_t o = (uint32_t)((k0 + key) * S::NB + db) * 34u;
-            const bool par = (o & 2u) != 0;
-            const uint32_t d16 = par ? (raw.k[i][0] >> 16) : (raw.k[i][0] & 0xffffu);
-            const h2_t d = as_h2(d16 | (d16 << 16));
-            uint32_t w[16];
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const uint32_t q = par ? raw.k[i][c + 1] : __builtin_amdgcn_alignbyte(raw.k[i][c + 1], raw.k[i][c], 2);
-                w[2 * c] = q8_pair<false>(q, d);
-                w[2 * c + 1] = q8_pair<true>(q, d);
-            }
-            u4_t* dst = reinterpret_cast<u4_t*>(Ks + key * KROW + db * 32);
-#pragma unroll
-            for (int c = 0; c < 4; c++) dst[c] = u4_t{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
-        } else {
-            const int v = u - S::KU;
-            const int kp = v % (kBKV / 2), dg = v / (kBKV / 2);
-            const int db = dg >> 1, hh = dg & 1;
-            uint32_t w[2][8];
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const uint32_t o = (uint32_t)((k0 + 2 * kp + e) * S::NB + db) * 34u;
-                const uint32_t sh = (o + 2u) & 3u;  // code bytes start 0 or 2 bytes into the first word
-                const uint32_t d16 = (o & 2u) ? (raw.v[i][6 * e] >> 16) : (raw.v[i][6 * e] & 0xffffu);
-                const h2_t d = as_h2(d16 | (d16 << 16));
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const uint32_t q = __builtin_amdgcn_alignbyte(raw.v[i][6 * e + 2 + c], raw.v[i][6 * e + 1 + c], sh);
-                    w[e][2 * c] = q8_pair<false>(q, d);
-                    w[e][2 * c + 1] = q8_pair<true>(q, d);
-                }
-            }
-            // w[e][c] = {V[key e][16dg + 2c], V[key e][16dg + 2c + 1]}
-            uint32_t* vt = reinterpret_cast<uint32_t*>(Vt);
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const int dd = 16 * dg + 2 * c;
-                vt[(dd * VROW + 2 * kp) >> 1] = perm(w[1][c], w[0][c], 0x05040100u);
-                vt[((dd + 1) * VROW + 2 * kp) >> 1] = perm(w[1][c], w[0][c], 0x07060302u);
-            }
-        }
-    }
 }
 
 // Staging from a dequantized fp16 cache: K' [H, Mp, D] (row-major) and V'^T
@@ -345,9 +231,8 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
 //    8 keys that lane supplies as the B operand of O^T = V^T . P^T.
 //  * fp32 running max / sum / output accumulators (the reference keeps S, P
 //    and O in half); the output is rounded to fp16 once.
-template <int D, bool F16>
+template <int D>
 __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(AttnParams p) {
-    using S = AttnStage<D>;
     constexpr int KROW = D + 8;                // LDS row (halfs) of K tile [key][d]
     constexpr int VROW = kBKV + 8;             // LDS row (halfs) of V^T tile [d][key]
     constexpr int DT = D / 32;                 // 32-row output tiles along d
@@ -375,25 +260,12 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
     const _Float16* Qh = p.Q + (size_t)h * head_elems;
     const int hk = p.Hkv ? h / ((int)p.H / (int)p.Hkv) : h;  // grouped-query: shared KV head
     const int Mp = (int)p.Mp;
-    __amdgpu_buffer_rsrc_t kr, vr;
-    if constexpr (F16) {
-        const uint32_t bytes = (uint32_t)((size_t)Mp * D * 2);
-        kr = make_rsrc(p.Kf + (size_t)hk * Mp * D, bytes);
-        vr = make_rsrc(p.Vtf + (size_t)hk * Mp * D, bytes);
-    } else {
-        const uint32_t kv_bytes = (uint32_t)(head_elems / 32 * 34);
-        kr = make_rsrc(p.Kq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
-        vr = make_rsrc(p.Vq + (size_t)hk * (head_elems / 32) * 34, kv_bytes);
-    }
-    using Raw = typename std::conditional<F16, AttnRawF16<D>, AttnRaw<D>>::type;
-    auto fetch = [&](int k0, Raw& raw) {
-        if constexpr (F16) attn_fetch_f16<D>(kr, vr, k0, Mp, tid, raw);
-        else attn_fetch<D>(kr, vr, k0, M, tid, raw);
-    };
-    auto stage = [&](const Raw& raw, int k0, _Float16* Kd, _Float16* Vd) {
-        if constexpr (F16) attn_stage_f16<D>(raw, tid, Kd, Vd);
-        else attn_stage<D>(raw, k0, tid, Kd, Vd);
-    };
+    const uint32_t bytes = (uint32_t)((size_t)Mp * D * 2);
+    auto kr = make_rsrc(p.Kf + (size_t)hk * Mp * D, bytes);
+    auto vr = make_rsrc(p.Vtf + (size_t)hk * Mp * D, bytes);
+    using Raw = AttnRawF16<D>;
+    auto fetch = [&](int k0, Raw& raw) { attn_fetch_f16<D>(kr, vr, k0, Mp, tid, raw); };
+    auto stage = [&](const Raw& raw, int k0, _Float16* Kd, _Float16* Vd) { attn_stage_f16<D>(raw, tid, Kd, Vd); };
 
     const int q_last = min(q0 + kBQ, M) - 1;
     const int ntiles = q_last / kBKV + 1;
@@ -843,25 +715,19 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
-    const bool f16 = p.Kf != nullptr;
-    if (f16 && (p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV)) return hipErrorInvalidValue;
+    // the kernels read the dequantized fp16 cache (launch_kv_prep)
+    if (p.Kf == nullptr || p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV) return hipErrorInvalidValue;
 #ifndef QR_ATTN_PAIR
 #define QR_ATTN_PAIR 1
 #endif
-    if (QR_ATTN_PAIR && f16 && p.D == 64) {
+    if (QR_ATTN_PAIR && p.D == 64) {
         const uint32_t qtiles = (p.M + kBQ - 1) / kBQ;
         hipLaunchKernelGGL((flash_attn_pair_kernel<64>), dim3(((qtiles + 1) / 2) * p.H), dim3(512), 0, st, p);
         return hipGetLastError();
     }
     switch (p.D) {
-        case 64:
-            if (f16) hipLaunchKernelGGL((flash_attn_q8_0_kernel<64, true>), grid, dim3(256), 0, st, p);
-            else hipLaunchKernelGGL((flash_attn_q8_0_kernel<64, false>), grid, dim3(256), 0, st, p);
-            break;
-        case 128:
-            if (f16) hipLaunchKernelGGL((flash_attn_q8_0_kernel<128, true>), grid, dim3(256), 0, st, p);
-            else hipLaunchKernelGGL((flash_attn_q8_0_kernel<128, false>), grid, dim3(256), 0, st, p);
-            break;
+        case 64: hipLaunchKernelGGL((flash_attn_q8_0_kernel<64>), grid, dim3(256), 0, st, p); break;
+        case 128: hipLaunchKernelGGL((flash_attn_q8_0_kernel<128>), grid, dim3(256), 0, st, p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -389,8 +389,7 @@ int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t 
     _Float16* kf = static_cast<_Float16*>(g_attn_ws);
     _Float16* vtf = kf + half_bytes / 2;
     hipError_t e = qr::launch_kv_prep(dk, dv, true, kf, vtf, Hkv, M, D, g_stream);
-    qr::AttnParams p{static_cast<const _Float16*>(dq), static_cast<const uint8_t*>(dk),
-                     static_cast<const uint8_t*>(dv), static_cast<_Float16*>(dout), H, M, D, scale,
+    qr::AttnParams p{static_cast<const _Float16*>(dq), static_cast<_Float16*>(dout), H, M, D, scale,
                      o_token_major ? 1 : 0, Hkv, kf, vtf, Mp};
     if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(p, g_stream);
     finish_outputs();
@@ -534,7 +533,7 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
         // Q8_0 KV cache (unified_prefill_engine.mm:554-572) as its dequantized
         // values: quantize + dequantize in registers, fp16 K and V^T out
         hipError_t e = qr::launch_kv_prep(k, v, false, kf, vtf, Hkv, M, D, g_stream);
-        qr::AttnParams ap{q, nullptr, nullptr, o, Hq, M, D, scale, 1, Hkv, kf, vtf, Mp};
+        qr::AttnParams ap{q, o, Hq, M, D, scale, 1, Hkv, kf, vtf, Mp};
         if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(ap, g_stream);
         rc = check(e, "layer attention");
     }

@@ -45,15 +45,13 @@ hipError_t launch_quantize_q8_0(const _Float16* src, uint8_t* dst, size_t num_bl
 
 struct AttnParams {
     const _Float16* Q;    // [H, M, D]
-    const uint8_t* Kq;    // Q8_0 blocks over [Hkv, M, D]
-    const uint8_t* Vq;    // Q8_0 blocks over [Hkv, M, D]
     _Float16* O;          // [H, M, D] or token-major [M, H * D]
     uint32_t H, M, D;
     float scale;
     int o_token_major;
     uint32_t Hkv;         // KV heads (grouped-query: query head h reads KV head h / (H / Hkv)); 0 = H
-    // Dequantized fp16 cache (launch_kv_prep) in place of Kq / Vq when Kf is
-    // set: Kf [Hkv, Mp, D], Vtf [Hkv, D, Mp], Mp = kv_padded_len(M).
+    // The dequantized fp16 cache of the Q8_0 K / V (launch_kv_prep):
+    // Kf [Hkv, Mp, D], Vtf [Hkv, D, Mp], Mp = kv_padded_len(M).
     const _Float16* Kf;
     const _Float16* Vtf;
     uint32_t Mp;
