@@ -18,6 +18,10 @@
 #include "qr_formats.h"
 #include "qr_kernels.h"
 
+#ifndef QR_LAYER_GROUPED_QKV
+#define QR_LAYER_GROUPED_QKV 1
+#endif
+
 namespace {
 
 std::mutex g_mu;
@@ -522,9 +526,28 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
                                       eps, norm_type, g_stream), "layer rmsnorm");
         a = xn;
     }
-    rc = rc ? rc : proj(a, Wq, nullptr, q, nullptr, HQ, dm, D);
-    rc = rc ? rc : proj(a, Wk, nullptr, k, nullptr, HK, dm, D);
-    rc = rc ? rc : proj(a, Wv, nullptr, v, nullptr, HK, dm, D);
+    // Q, K, V: one grouped launch when the three fit one grid, else three
+    if (!rc) {
+        qr::GemmParams g{};
+        g.format = format;
+        g.X = static_cast<const _Float16*>(a);
+        g.W = static_cast<const uint8_t*>(Wq);
+        g.Y = q;
+        g.M = M; g.N = HQ; g.K = dm;
+        g.head_D = D;
+        g.col_bytes = qr::kernel_weight_bytes(format, dm, HQ) / HQ;
+        g.ngroups = 3;
+        g.Wx[0] = static_cast<const uint8_t*>(Wk); g.Yx[0] = k; g.Nx[0] = HK;
+        g.Wx[1] = static_cast<const uint8_t*>(Wv); g.Yx[1] = v; g.Nx[1] = HK;
+        if (QR_LAYER_GROUPED_QKV && qr::gemm_grouped_ok(g)) {
+            g.ksplit = 1;
+            rc = check(qr::launch_gemm(g, g_stream), "layer qkv");
+        } else {
+            rc = proj(a, Wq, nullptr, q, nullptr, HQ, dm, D);
+            rc = rc ? rc : proj(a, Wk, nullptr, k, nullptr, HK, dm, D);
+            rc = rc ? rc : proj(a, Wv, nullptr, v, nullptr, HK, dm, D);
+        }
+    }
     if (!rc && rope) {
         rc = check(qr::launch_rope(q, Hq, M, D, theta, offset, traditional, g_stream), "layer rope");
         rc = rc ? rc : check(qr::launch_rope(k, Hkv, M, D, theta, offset, traditional, g_stream), "layer rope");

@@ -112,10 +112,25 @@ gemm_rb_kernel(GemmParams p) {
     const int h = lane >> 5;     // quant group of the step this lane owns
     const int c32 = lane & 31;
 
+    // grouped launch: the group of this workgroup's tile takes over W / Y / N
+    uint32_t bid = blockIdx.x;
+    if (p.ngroups > 1) {
+        const uint32_t ntm = (p.M + C::BM - 1) / C::BM;
+        const uint32_t t0 = ntm * ((p.N + C::BN - 1) / C::BN);
+        if (bid >= t0) {
+            bid -= t0;
+            const uint32_t t1 = ntm * ((p.Nx[0] + C::BN - 1) / C::BN);
+            const int gx = (bid < t1 || p.ngroups == 2) ? 0 : 1;
+            if (gx == 1) bid -= t1;
+            p.W = p.Wx[gx];
+            p.Y = p.Yx[gx];
+            p.N = p.Nx[gx];
+        }
+    }
     const uint32_t M = p.M, N = p.N, K = p.K;
     const uint32_t nt_m = (M + C::BM - 1) / C::BM, nt_n = (N + C::BN - 1) / C::BN;
     uint32_t tmi, tni;
-    rb::tile_of(blockIdx.x, nt_m, nt_n, p.group_m, tmi, tni);
+    rb::tile_of(bid, nt_m, nt_n, p.group_m, tmi, tni);
     const int m0 = tmi * C::BM, n0 = tni * C::BN;
     const uint32_t ksplit = p.ksplit ? p.ksplit : 1;
     const uint32_t kz = blockIdx.y;
@@ -477,7 +492,9 @@ static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES, true>
                              : gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES, false>;
     const size_t lds = C::LDS_BYTES;
-    const uint32_t T = ((p.M + C::BM - 1) / C::BM) * ((p.N + C::BN - 1) / C::BN);
+    const uint32_t ntm = (p.M + C::BM - 1) / C::BM;
+    uint32_t T = ntm * ((p.N + C::BN - 1) / C::BN);
+    for (uint32_t g = 1; g < p.ngroups && g < 3; g++) T += ntm * ((p.Nx[g - 1] + C::BN - 1) / C::BN);
     const uint32_t ks = p.ksplit ? p.ksplit : 1;
     hipLaunchKernelGGL(kern, dim3(T, ks), dim3(C::NT), lds, st, p);
     return hipGetLastError();

@@ -20,9 +20,25 @@ hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
     }
 }
 
+static uint32_t tiles_of(const GemmParams& p, const RbShape& d) {
+    const uint32_t ntm = (p.M + d.bm - 1) / d.bm;
+    uint32_t T = ntm * ((p.N + d.bn - 1) / d.bn);
+    for (uint32_t g = 1; g < p.ngroups && g < 3; g++) T += ntm * ((p.Nx[g - 1] + d.bn - 1) / d.bn);
+    return T;
+}
+
+bool gemm_grouped_ok(const GemmParams& p) {
+    if (p.ngroups < 2 || p.ngroups > 3 || p.W2 || p.R) return false;
+    // every group must take the shape group 0 takes, and the grid needs no K split
+    const int s0 = rb_pick(p.format, p.M, p.N, false);
+    for (uint32_t g = 1; g < p.ngroups; g++)
+        if (rb_pick(p.format, p.M, p.Nx[g - 1], false) != s0) return false;
+    return gemm_pick_ksplit(p) == 1;
+}
+
 uint32_t gemm_pick_ksplit(const GemmParams& p) {
     const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.W2 != nullptr));
-    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+    const uint32_t T = tiles_of(p, d);
     // One workgroup fits a CU (its registers), so the grid runs in waves of
     // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
     // >= 512 of K per split) while the grid still fits one such wave.

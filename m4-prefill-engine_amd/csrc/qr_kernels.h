@@ -23,11 +23,20 @@ struct GemmParams {
     float* ws;
     uint32_t* counters;
     uint32_t group_m;     // row-tiles per XCD tile group (0: kernel default)
+    // Grouped launch: up to two more projections of the same X (same K,
+    // format, head_D; no residual, no SwiGLU, no K split) in the same grid,
+    // group g >= 1 writing Yx[g - 1] [M, Nx[g - 1]] from Wx[g - 1].
+    uint32_t ngroups;     // 0 or 1: a single projection
+    const uint8_t* Wx[2];
+    _Float16* Yx[2];
+    uint32_t Nx[2];
 };
 
 hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
 uint32_t gemm_group_m(const GemmParams& p);
 uint32_t gemm_pick_ksplit(const GemmParams& p);
+// Whether launch_gemm can run p's groups (ngroups >= 2) as one grid.
+bool gemm_grouped_ok(const GemmParams& p);
 size_t gemm_workspace_floats(const GemmParams& p, uint32_t ksplit, uint32_t* tiles);
 
 // Small-M weight-streaming projection (M <= 64, no SwiGLU).  `ws` holds
