@@ -32,59 +32,50 @@ namespace qr {
 __device__ __forceinline__ uint32_t lds32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
 // A-operand fragment of one 32-element group, read from a weight strip in LDS
-// (16-byte aligned).  Lane group g = lane / 16 holds elements 8g .. 8g+7.
+// (16-byte aligned).  Lane group g = lane / 16 holds elements 8g .. 8g+7, or for
+// formats with kNibbleOrder elements 4g .. 4g+3 and 16+4g .. 19+4g.
 // load() reads the raw words of one lane from LDS; decode() is lane-local.
 template <int F> struct Frag;
 
-// Q4_0: elements 8g..8g+7 are the low (g < 2) or high (g >= 2) nibbles of
-// code bytes 8(g&1) .. 8(g&1)+7, read as three aligned dwords plus a byte
-// funnel shift (18-byte groups are only 2-byte aligned), and the dword that
-// holds the scale.
+// Q4_0 (18-byte groups, 2-byte aligned): lane group g takes code bytes
+// 4g .. 4g + 3, i.e. elements 4g .. 4g + 3 (low nibbles) and 16 + 4g .. 19 + 4g
+// (high nibbles) -- kNibbleOrder: the activations are read in the same order.
+// Its code dword sits at a wave-uniform byte shift from the aligned pair of
+// dwords read; a third read fetches the dword holding the scale.
 template <> struct Frag<QUANT_Q4_0> {
-    static constexpr int kRaw = 4;
-    __device__ static uint32_t start(uint32_t kb, int g) { return kb * 18u + ((g & 1) ? 10u : 0u); }
-    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[4]) {
-        const uint8_t* p = strip + (start(kb, g) & ~3u);
-        raw[0] = lds32(p); raw[1] = lds32(p + 4); raw[2] = lds32(p + 8);
-        raw[3] = lds32(strip + ((kb * 18u) & ~3u));  // dword holding the scale
+    static constexpr int kRaw = 3;
+    static constexpr bool kNibbleOrder = true;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[3]) {
+        const uint8_t* p = strip + ((kb * 18u + 2u + 4u * (uint32_t)g) & ~3u);
+        raw[0] = lds32(p); raw[1] = lds32(p + 4);
+        raw[2] = lds32(strip + ((kb * 18u) & ~3u));  // dword holding the scale
     }
-    __device__ static h8_t decode(const uint32_t raw[4], uint32_t kb, int g) {
-        const uint32_t sh = start(kb, g) & 2u;
-        const uint32_t v0 = sh ? __builtin_amdgcn_alignbyte(raw[1], raw[0], 2) : raw[0];
-        const uint32_t v1 = sh ? __builtin_amdgcn_alignbyte(raw[2], raw[1], 2) : raw[1];
-        const uint32_t v2 = sh ? (raw[2] >> 16) : raw[2];
-        uint32_t q0, q1;
-        if (g & 1) {
-            q0 = v0; q1 = v1;
-        } else {
-            q0 = __builtin_amdgcn_alignbyte(v1, v0, 2);
-            q1 = __builtin_amdgcn_alignbyte(v2, v1, 2);
-        }
-        const uint32_t d16 = ((kb * 18u) & 2u) ? (raw[3] >> 16) : (raw[3] & 0xffffu);
-        if (g >= 2) { q0 >>= 4; q1 >>= 4; }
-        q0 &= 0x0f0f0f0fu;
-        q1 &= 0x0f0f0f0fu;
+    __device__ static h8_t decode(const uint32_t raw[3], uint32_t kb, int) {
+        const uint32_t w = __builtin_amdgcn_alignbyte(raw[1], raw[0], (kb * 18u + 2u) & 2u);
+        const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+        const uint32_t d16 = ((kb * 18u) & 2u) ? (raw[2] >> 16) : (raw[2] & 0xffffu);
         const h2_t d = as_h2(d16 | (d16 << 16));
-        u4_t w;
+        u4_t o;
         if (__all(__builtin_fabsf(h2f(d16)) <= kQ4_0FastMaxScale)) {  // fma(q, d, -8d): -8d exact
             const h2_t m8 = {(_Float16)-8.0f, (_Float16)-8.0f};
             const h2_t c = d * m8;
-            w = u4_t{as_u32(__builtin_elementwise_fma(code_pair<false>(q0), d, c)),
-                     as_u32(__builtin_elementwise_fma(code_pair<true>(q0), d, c)),
-                     as_u32(__builtin_elementwise_fma(code_pair<false>(q1), d, c)),
-                     as_u32(__builtin_elementwise_fma(code_pair<true>(q1), d, c))};
+            o = u4_t{as_u32(__builtin_elementwise_fma(code_pair<false>(lo), d, c)),
+                     as_u32(__builtin_elementwise_fma(code_pair<true>(lo), d, c)),
+                     as_u32(__builtin_elementwise_fma(code_pair<false>(hi), d, c)),
+                     as_u32(__builtin_elementwise_fma(code_pair<true>(hi), d, c))};
         } else {  // (q - 8) * d
             const h2_t off = {(_Float16)8.0f, (_Float16)8.0f};
-            w = u4_t{as_u32((code_pair<false>(q0) - off) * d), as_u32((code_pair<true>(q0) - off) * d),
-                     as_u32((code_pair<false>(q1) - off) * d), as_u32((code_pair<true>(q1) - off) * d)};
+            o = u4_t{as_u32((code_pair<false>(lo) - off) * d), as_u32((code_pair<true>(lo) - off) * d),
+                     as_u32((code_pair<false>(hi) - off) * d), as_u32((code_pair<true>(hi) - off) * d)};
         }
-        return __builtin_bit_cast(h8_t, w);
+        return __builtin_bit_cast(h8_t, o);
     }
 };
 
 // MLX_4BIT (20-byte groups, dword aligned): every lane reads {d, bias} and
 // its two code dwords (codes 0..7 for g&1 == 0, 8..15 for g&1 == 1).
 template <> struct Frag<QUANT_MLX_4BIT> {
+    static constexpr bool kNibbleOrder = false;
     static constexpr int kRaw = 3;
     __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[3]) {
         // raw = {d | bias, code dwords 2(g&1), 2(g&1)+1}
@@ -113,6 +104,7 @@ template <> struct Frag<QUANT_MLX_4BIT> {
 // Q4_K: group kb is sub-block s = kb % 8 of super-block kb / 8.  Every lane
 // reads the 16-byte header and its 8 code bytes 16s + 8(g&1) .. +7.
 template <> struct Frag<QUANT_Q4_K> {
+    static constexpr bool kNibbleOrder = false;
     static constexpr int kRaw = 6;
     __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[6]) {
         const uint8_t* p = strip + (kb >> 3) * 144u;
@@ -155,6 +147,7 @@ template <> struct Frag<QUANT_Q4_K> {
 // TERNARY_1_58 (12-byte groups): elements 8g..8g+7 are the 16-bit field
 // 16(g&1) of code word g/2.  w = (1024 + c - 1025) * d, exact.
 template <> struct Frag<QUANT_TERNARY_1_58> {
+    static constexpr bool kNibbleOrder = false;
     static constexpr int kRaw = 2;
     __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
         const uint8_t* p = strip + kb * 12u;
@@ -230,7 +223,7 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
     constexpr uint32_t SB = GPW * kSkWaves * GB;      // strip bytes (multiple of 16)
     static_assert(SB % 16 == 0, "strip bytes must be a multiple of 16");
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r16 = lane & 15;
     const uint32_t cg = blockIdx.x, ks = blockIdx.y;
     const uint32_t M = p.M, N = p.N, K = p.K;
@@ -295,7 +288,13 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t m = min(16u * mt + r16, M - 1);  // rows >= M are zeroed below
-            xf[b][mt] = *reinterpret_cast<const u4_t*>(xs + m * L.xrs + (kb * 32u + 8u * g) * 2u);
+            if constexpr (FR::kNibbleOrder) {  // k = 4g .. 4g + 3, 16 + 4g .. 19 + 4g
+                const uint8_t* px = xs + m * L.xrs + (kb * 32u + 4u * g) * 2u;
+                const u2_t lo = *reinterpret_cast<const u2_t*>(px), hi = *reinterpret_cast<const u2_t*>(px + 32);
+                xf[b][mt] = u4_t{lo.x, lo.y, hi.x, hi.y};
+            } else {  // k = 8g .. 8g + 7
+                xf[b][mt] = *reinterpret_cast<const u4_t*>(xs + m * L.xrs + (kb * 32u + 8u * g) * 2u);
+            }
         }
 #pragma unroll
         for (int t = 0; t < kSkNT; t++) FR::load(wsb + (16u * t + r16) * L.sbp, kb, g, raw[b][t]);
