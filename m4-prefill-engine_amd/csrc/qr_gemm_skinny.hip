@@ -72,51 +72,46 @@ template <> struct Frag<QUANT_Q4_0> {
     }
 };
 
-// MLX_4BIT (20-byte groups, dword aligned): every lane reads {d, bias} and
-// its two code dwords (codes 0..7 for g&1 == 0, 8..15 for g&1 == 1).
+// MLX_4BIT (20-byte groups, dword aligned), nibble order: every lane reads
+// {d, bias} and code dword g (elements 4g .. 4g+3 low, 16+4g .. 19+4g high).
 template <> struct Frag<QUANT_MLX_4BIT> {
-    static constexpr bool kNibbleOrder = false;
-    static constexpr int kRaw = 3;
-    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[3]) {
-        // raw = {d | bias, code dwords 2(g&1), 2(g&1)+1}
+    static constexpr bool kNibbleOrder = true;
+    static constexpr int kRaw = 2;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
         const uint8_t* p = strip + kb * 20u;
         raw[0] = lds32(p);
-        raw[1] = lds32(p + 4u + 8u * (uint32_t)(g & 1));
-        raw[2] = lds32(p + 8u + 8u * (uint32_t)(g & 1));
+        raw[1] = lds32(p + 4u + 4u * (uint32_t)g);
     }
-    __device__ static h8_t decode(const uint32_t raw[3], uint32_t, int g) {
+    __device__ static h8_t decode(const uint32_t raw[2], uint32_t, int) {
         const uint32_t db = raw[0];
-        uint32_t q0 = raw[1];
-        uint32_t q1 = raw[2];
-        if (g >= 2) { q0 >>= 4; q1 >>= 4; }
-        q0 &= 0x0f0f0f0fu;
-        q1 &= 0x0f0f0f0fu;
+        const uint32_t lo = raw[1] & 0x0f0f0f0fu, hi = (raw[1] >> 4) & 0x0f0f0f0fu;
         const uint32_t d16 = db & 0xffffu, b16 = db >> 16;
         const h2_t d = as_h2(d16 | (d16 << 16)), bias = as_h2(b16 | (b16 << 16));
-        u4_t w = {as_u32(__builtin_elementwise_fma(code_pair<false>(q0), d, bias)),
-                  as_u32(__builtin_elementwise_fma(code_pair<true>(q0), d, bias)),
-                  as_u32(__builtin_elementwise_fma(code_pair<false>(q1), d, bias)),
-                  as_u32(__builtin_elementwise_fma(code_pair<true>(q1), d, bias))};
+        u4_t w = {as_u32(__builtin_elementwise_fma(code_pair<false>(lo), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<true>(lo), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<false>(hi), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<true>(hi), d, bias))};
         return __builtin_bit_cast(h8_t, w);
     }
 };
 
 // Q4_K: group kb is sub-block s = kb % 8 of super-block kb / 8.  Every lane
-// reads the 16-byte header and its 8 code bytes 16s + 8(g&1) .. +7.
+// reads the 16-byte header and, in nibble order, code dword g of the
+// sub-block (bytes 16s + 4g .. +3).
 template <> struct Frag<QUANT_Q4_K> {
-    static constexpr bool kNibbleOrder = false;
-    static constexpr int kRaw = 6;
-    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[6]) {
+    static constexpr bool kNibbleOrder = true;
+    static constexpr int kRaw = 5;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[5]) {
         const uint8_t* p = strip + (kb >> 3) * 144u;
         u4_t h = *reinterpret_cast<const u4_t*>(p);
-        u2_t q = *reinterpret_cast<const u2_t*>(p + 16u + 16u * (kb & 7u) + 8u * (uint32_t)(g & 1));
-        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w; raw[4] = q.x; raw[5] = q.y;
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = lds32(p + 16u + 16u * (kb & 7u) + 4u * (uint32_t)g);
     }
     __device__ static int binade(uint32_t h16) {
         int e = (int)((h16 >> 10) & 0x1f);
         return (e < 1 ? 1 : e) - 15;
     }
-    __device__ static h8_t decode(const uint32_t raw[6], uint32_t kb, int g) {
+    __device__ static h8_t decode(const uint32_t raw[5], uint32_t kb, int) {
         const uint32_t s = kb & 7u;
         const uint32_t d16 = raw[0] & 0xffffu, dm16 = raw[0] >> 16;
         const uint64_t s07 = (uint64_t)raw[1] | ((uint64_t)raw[2] << 32);
@@ -128,10 +123,7 @@ template <> struct Frag<QUANT_Q4_K> {
         const float B = h2f(dm16) * (float)mn;
         const int gap = binade(d16) - binade(dm16);
         const bool fast = (A == 0.0f) || (B == 0.0f) || (gap <= 3 && gap >= -7);
-        uint32_t q0 = raw[4], q1 = raw[5];
-        if (g >= 2) { q0 >>= 4; q1 >>= 4; }
-        q0 &= 0x0f0f0f0fu;
-        q1 &= 0x0f0f0f0fu;
+        const uint32_t q0 = raw[4] & 0x0f0f0f0fu, q1 = (raw[4] >> 4) & 0x0f0f0f0fu;
         u4_t w;
         if (__all(fast)) {  // exact-sum path only when some lane needs it
             w = u4_t{affine_pair_exact(code_pair<false>(q0), A, -B), affine_pair_exact(code_pair<true>(q0), A, -B),
