@@ -96,6 +96,21 @@ M4_API int m4_bridge_dispatch_head_gemm(void* X_ptr, size_t X_bytes, void* W_ptr
                                  size_t Y_bytes, int format, uint32_t M, uint32_t H, uint32_t D,
                                  uint32_t K);
 
+/* A router kernel by its Metal pipeline name, with that kernel's buffer and
+ * constant slots: A = X (buffer 0), B = W (1), C = Y (2), and dims = the
+ * constants from slot 3 on -- {M, N, K} for quant_router_gemm_<fmt>_64x64
+ * (quant_router_kernels.metal:588-750) and {M, H, D, K} for
+ * quant_router_head_gemm_<fmt>_64x64 (:754-927); kernel names as listed by the
+ * registry (src/router/quant_registry.mm:60-172).  The vector-ALU ternary
+ * kernels quant_router_gemm_ternary_1_58_vec (:934-1064) and
+ * quant_router_head_gemm_ternary_1_58_vec (:1067-1201) compute the same
+ * projection and run the matrix-core path here.  Returns -3 for an unknown
+ * name, -4 when ndims does not match the kernel's constant slots, otherwise
+ * what dispatch_router_gemm / dispatch_head_gemm return. */
+M4_API int m4_bridge_dispatch_router_kernel(const char* kernel_name, void* X_ptr, size_t X_bytes, void* W_ptr,
+                                            size_t W_bytes, void* Y_ptr, size_t Y_bytes, const uint32_t* dims,
+                                            uint32_t ndims);
+
 /* Projection with a fused residual: Y = fp16(X . W^T + R), R fp16 [M, N];
  * replaces a GEMM followed by vector_add_residual (unified_kernels.metal:
  * 78-88; unified_prefill_engine.mm:183-186).  Y may alias R. */

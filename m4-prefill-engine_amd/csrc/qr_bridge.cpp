@@ -17,6 +17,7 @@
 #include "../../include/m4_mlx_bridge.h"
 #include "qr_formats.h"
 #include "qr_kernels.h"
+#include "qr_registry.h"
 
 #ifndef QR_LAYER_GROUPED_QKV
 #define QR_LAYER_GROUPED_QKV 1
@@ -300,6 +301,40 @@ int m4_bridge_dispatch_head_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y
     if (!g_initialized) return -1;
     if (H == 0 || D == 0) return -4;
     return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, H * D, D, true);
+}
+
+int m4_bridge_dispatch_router_kernel(const char* kernel_name, void* X, size_t Xb, void* W, size_t Wb, void* Y,
+                                     size_t Yb, const uint32_t* dims, uint32_t ndims) {
+    if (!g_initialized) return -1;
+    if (!kernel_name || !dims) return -2;
+    const std::string name(kernel_name);
+    // The vector-ALU ternary kernels compute the same projection as the
+    // matrix-core ones (quant_router_kernels.metal:934-1201); here both names
+    // run the MFMA path.
+    int format = -1;
+    bool head = false;
+    if (name == "quant_router_gemm_ternary_1_58_vec") {
+        format = qr::QUANT_TERNARY_1_58;
+    } else if (name == "quant_router_head_gemm_ternary_1_58_vec") {
+        format = qr::QUANT_TERNARY_1_58;
+        head = true;
+    } else {
+        auto& reg = qr::QuantRegistry::instance();
+        for (qr::QuantFormat f : reg.available_formats()) {
+            const qr::QuantCodecDescriptor* d = reg.get(f);
+            if (!d) continue;
+            if (d->gemm_kernel_name == name) format = (int)f;
+            else if (d->head_gemm_kernel_name == name) { format = (int)f; head = true; }
+            if (format >= 0) break;
+        }
+    }
+    if (format < 0 || !has_kernels(format)) return -3;
+    if (head) {  // constant slots M, H, D, K
+        if (ndims != 4) return -4;
+        return m4_bridge_dispatch_head_gemm(X, Xb, W, Wb, Y, Yb, format, dims[0], dims[1], dims[2], dims[3]);
+    }
+    if (ndims != 3) return -4;  // constant slots M, N, K
+    return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, dims[0], dims[2], dims[1], 0, true);
 }
 
 int m4_bridge_dispatch_gemm_residual(void* X, size_t Xb, void* W, size_t Wb, void* R, size_t Rb, void* Y, size_t Yb,

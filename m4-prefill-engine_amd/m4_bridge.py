@@ -64,6 +64,8 @@ SIGNATURES = {
     "m4_bridge_validate_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_router_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_head_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32, _U32], _I),
+    "m4_bridge_dispatch_router_kernel": ([ctypes.c_char_p, _VP, _SZ, _VP, _SZ, _VP, _SZ,
+                                          ctypes.POINTER(ctypes.c_uint32), _U32], _I),
     "m4_bridge_dispatch_gemm_residual": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_swiglu": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_quantize_kv_q8_0": ([_VP, _SZ, _VP, _SZ, ctypes.c_uint64], _I),
@@ -278,6 +280,24 @@ class HIPBridge:
         ret = self._lib.m4_bridge_dispatch_head_gemm(a[0][0], a[0][1], a[1][0], a[1][1], a[2][0], a[2][1],
                                                      int(format), M, H, D, K)
         self._check("m4_bridge_dispatch_head_gemm", ret)
+        self._in_flight_tensors.append((X, W, Y))
+        if check_finite:
+            self._pending_finite_checks.append(Y)
+        return ret
+
+    def dispatch_router_kernel(self, kernel_name: str, X, W, Y, *dims, check_finite: bool = False) -> int:
+        """A router kernel by its Metal pipeline name with that kernel's slots:
+        buffers A = X, B = W, C = Y, then the constants -- (M, N, K) for
+        quant_router_gemm_<fmt>_64x64, (M, H, D, K) for the head kernels
+        (quant_router_kernels.metal:588-927).  The vector-ALU ternary names
+        quant_router_{,head_}gemm_ternary_1_58_vec (:934-1201) compute the same
+        projection on the matrix-core path."""
+        a = [self.extract_buffer_address_and_size(t) for t in (X, W, Y)]
+        self._bind_stream(X, W, Y)
+        arr = (ctypes.c_uint32 * max(len(dims), 1))(*[int(d) for d in dims])
+        ret = self._lib.m4_bridge_dispatch_router_kernel(kernel_name.encode(), a[0][0], a[0][1], a[1][0], a[1][1],
+                                                         a[2][0], a[2][1], arr, len(dims))
+        self._check("m4_bridge_dispatch_router_kernel", ret)
         self._in_flight_tensors.append((X, W, Y))
         if check_finite:
             self._pending_finite_checks.append(Y)

@@ -141,6 +141,9 @@ def test_uninitialized_bridge_refuses_work(lib):
     assert lib.m4_bridge_rmsnorm(x.ctypes.data, x.nbytes, w.ctypes.data, 256, x.ctypes.data, x.nbytes, 64, 128,
                                  1e-5, 1) == -1
     assert lib.m4_bridge_rope(x.ctypes.data, x.nbytes, 1, 64, 128, 1e4, 0, 0) == -1
+    dims = (ctypes.c_uint32 * 3)(64, 64, 128)
+    assert lib.m4_bridge_dispatch_router_kernel(b"quant_router_gemm_ternary_1_58_vec", x.ctypes.data, x.nbytes,
+                                                w.ctypes.data, w.nbytes, y.ctypes.data, y.nbytes, dims, 3) == -1
     assert lib.m4_bridge_dispatch_flash_attn_q8_0_gqa(x.ctypes.data, x.nbytes, w.ctypes.data, w.nbytes,
                                                       w.ctypes.data, w.nbytes, y.ctypes.data, y.nbytes,
                                                       2, 1, 32, 64, 0.125, 0) == -1

@@ -133,6 +133,47 @@ def test_gemm_var_rate_and_exl3(bridge, oracle, fmt, M, K, N):
     tolerance.check(host(Yh), refh, tolerance.gemm_bound(refh, axw.reshape(M, H, D).transpose(1, 0, 2), K))
 
 
+def test_router_kernels_by_name(bridge, oracle):
+    """Every router kernel name (quant_router_{,head_}gemm_<fmt>_64x64 from the
+    registry, quant_router_kernels.metal:588-927) and the vector-ALU ternary
+    names (:934-1201) with the kernels' constant slots give the same output as
+    the format-id entry points; the ternary names also meet the oracle bound.
+    Unknown names return -3, a wrong slot count -4."""
+    M, K, N, D = 33, 512, 128, 64
+    X = synth.activations(M, K, 91, std=0.35)
+    for fmt, sym in [(0, "q4_0"), (1, "mlx_4bit"), (2, "q4_k"), (3, "ternary_1_58"), (4, "var_rate_affine"),
+                     (5, "exl3"), (6, "q8_0"), (7, "prism_q2_0")]:
+        W = dev(synth.random_blocks(fmt, N, K, 92 + fmt))
+        names = [(f"quant_router_gemm_{sym}_64x64", False), (f"quant_router_head_gemm_{sym}_64x64", True)]
+        if fmt == 3:
+            names += [("quant_router_gemm_ternary_1_58_vec", False), ("quant_router_head_gemm_ternary_1_58_vec", True)]
+        Yf = empty16(M, N)
+        bridge.dispatch_router_gemm(dev(X), W, Yf, fmt, M, K, N)
+        Yhf = empty16(N // D, M, D)
+        bridge.dispatch_head_gemm(dev(X), W, Yhf, fmt, M, N // D, D, K)
+        for name, head in names:
+            if head:
+                Y = empty16(N // D, M, D)
+                bridge.dispatch_router_kernel(name, dev(X), W, Y, M, N // D, D, K)
+                bridge.synchronize()
+                assert np.array_equal(host(Y).view(np.uint16), host(Yhf).view(np.uint16)), name
+            else:
+                Y = empty16(M, N)
+                bridge.dispatch_router_kernel(name, dev(X), W, Y, M, N, K)
+                bridge.synchronize()
+                assert np.array_equal(host(Y).view(np.uint16), host(Yf).view(np.uint16)), name
+        if fmt == 3:
+            Wh = host(W)
+            ref = oracle.gemm(3, X, Wh, N)
+            tolerance.check(host(Yf), ref, tolerance.gemm_bound(ref, absxw(oracle, 3, X, Wh, K, N), K))
+    W = dev(synth.random_blocks(0, N, K, 99))
+    Y = empty16(M, N)
+    with pytest.raises(RuntimeError, match="status code -3"):
+        bridge.dispatch_router_kernel("quant_router_gemm_q5_0_64x64", dev(X), W, Y, M, N, K)
+    with pytest.raises(RuntimeError, match="status code -4"):
+        bridge.dispatch_router_kernel("quant_router_head_gemm_q4_0_64x64", dev(X), W, Y, M, N, K)
+
+
 def test_gemm_q4_0_scales_beyond_fast_path(bridge, oracle):
     """Q4_0 scales with |d| > 8188 (-8 d is not finite in binary16): the tiled
     kernel's fused fma(q, d, -8 d) decode cannot form them, so the wave takes
