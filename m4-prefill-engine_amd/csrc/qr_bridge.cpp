@@ -8,6 +8,10 @@
 // through bridge-owned device memory.
 #include <hip/hip_runtime.h>
 
+#include <sys/uio.h>
+#include <unistd.h>
+
+#include <cerrno>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -34,8 +38,9 @@ std::string g_last_error;
 
 struct Staged {
     void* dev;
-    void* host;      // non-null: copy dev -> host at synchronize
+    void* host;      // non-null: copy dev -> host at synchronize (once armed)
     size_t bytes;
+    bool armed;      // set once the dispatch that staged it has launched its kernels
 };
 std::vector<Staged> g_staged;      // freed at synchronize
 size_t g_staged_bytes = 0;
@@ -68,6 +73,46 @@ void* device_view(void* p) {
     return nullptr;
 }
 
+// Whether every page of the host range [p, p + bytes) can be read (and, for
+// outputs, written) by this process.  The reference wraps host memory with
+// newBufferWithBytesNoCopy and returns -5 when that fails for a range running
+// into an unmapped or protected page (tests/redteam_bridge.py:178-221); here
+// the staging copy would fault instead, so the range is probed first: one byte
+// per page through process_vm_readv / process_vm_writev on this process,
+// which report EFAULT rather than raising a signal.  Where the calls are not
+// permitted at all the probe is skipped.
+bool host_range_ok(const void* p, size_t bytes, bool write) {
+    if (bytes == 0) return true;
+    const uintptr_t pg = (uintptr_t)sysconf(_SC_PAGESIZE);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p), e = a + bytes - 1;
+    constexpr int kBatch = 512;
+    char tmp[kBatch];
+    struct iovec loc[kBatch], rem[kBatch];
+    // probe addresses: a, then the first byte of every later page up to e
+    uintptr_t q = a;
+    bool more = true;
+    while (more) {
+        int n = 0;
+        for (; n < kBatch && more; n++) {
+            loc[n] = {tmp + n, 1};
+            rem[n] = {reinterpret_cast<void*>(q), 1};
+            const uintptr_t next = (q / pg + 1) * pg;
+            more = next > q && next <= e;
+            q = next;
+        }
+        errno = 0;
+        ssize_t got = process_vm_readv(getpid(), loc, n, rem, n, 0);
+        if (got < 0 && errno != EFAULT) return true;  // probe unavailable
+        if (got != n) return false;
+        if (write) {
+            got = process_vm_writev(getpid(), loc, n, rem, n, 0);  // the bytes just read, unchanged
+            if (got < 0 && errno != EFAULT) return true;
+            if (got != n) return false;
+        }
+    }
+    return true;
+}
+
 // Device pointer usable by the kernels for buffer `p`: the pointer itself if it
 // is device memory aligned to `align`, else a staged copy.  For outputs
 // (`out`), the staged copy is written back at synchronize.  Returns null on
@@ -75,6 +120,10 @@ void* device_view(void* p) {
 void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
     void* d = device_view(p);
     if (d && (reinterpret_cast<uintptr_t>(d) % align) == 0) return d;
+    if (!d && !host_range_ok(p, bytes, out)) {
+        g_last_error = "host buffer range is not accessible";
+        return nullptr;
+    }
     void* s = nullptr;
     hipError_t e = hipMalloc(&s, bytes ? bytes : 16);
     if (e != hipSuccess) {
@@ -92,7 +141,7 @@ void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
     }
     // Device outputs that were only misaligned are copied back on the stream
     // right after the kernel (see finish_outputs); host outputs at synchronize.
-    g_staged.push_back({s, out ? p : nullptr, bytes});
+    g_staged.push_back({s, out ? p : nullptr, bytes, false});
     g_staged_bytes += bytes;
     return s;
 }
@@ -101,6 +150,8 @@ void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
 // (misaligned) are copied back in stream order.
 void finish_outputs() {
     for (auto& st : g_staged) {
+        if (st.armed) continue;
+        st.armed = true;  // a dispatch that fails before its launches never arms its outputs
         if (!st.host) continue;
         void* d = device_view(st.host);
         if (d) {
@@ -110,12 +161,23 @@ void finish_outputs() {
     }
 }
 
+// A dispatch whose buffers could not all be staged returns -5 before any
+// launch: the outputs it staged are never copied back.
+int staging_failed() {
+    for (auto& st : g_staged)
+        if (!st.armed) {
+            st.armed = true;
+            st.host = nullptr;
+        }
+    return -5;
+}
+
 void sync_and_release() {
     if (!g_stream) return;
     hipError_t e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) set_error("hipStreamSynchronize", e);
     for (auto& st : g_staged) {
-        if (st.host) {
+        if (st.host && st.armed) {
             e = hipMemcpy(st.host, st.dev, st.bytes, hipMemcpyDeviceToHost);
             if (e != hipSuccess) set_error("hipMemcpy(stage out)", e);
         }
@@ -190,7 +252,7 @@ int launch(const qr::GemmParams& p0) {
         hipError_t e = ensure_skinny_ws(floats ? floats : 1, groups);
         if (e != hipSuccess) {
             set_error("hipMalloc(split-K workspace)", e);
-            return -5;
+            return staging_failed();
         }
         e = qr::launch_gemm_skinny(p, g_sk_ws, g_sk_cnt, g_stream);
         if (e != hipSuccess) {
@@ -206,7 +268,7 @@ int launch(const qr::GemmParams& p0) {
         hipError_t e = ensure_skinny_ws(floats, tiles);
         if (e != hipSuccess) {
             set_error("hipMalloc(split-K workspace)", e);
-            return -5;
+            return staging_failed();
         }
         p.ws = g_sk_ws;
         p.counters = g_sk_cnt;
@@ -231,7 +293,7 @@ int gemm_common(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, void
     void* dw = resolve(W, wbytes, 16, true, false);
     void* dr = R ? resolve(R, (size_t)M * N * 2, 2, true, false) : nullptr;
     void* dy = resolve(Y, (size_t)M * N * 2, 2, false, true);
-    if (!dx || !dw || !dy || (R && !dr)) return -5;
+    if (!dx || !dw || !dy || (R && !dr)) return staging_failed();
     qr::GemmParams p{};
     p.format = format;
     p.X = static_cast<const _Float16*>(dx);
@@ -358,7 +420,7 @@ int m4_bridge_dispatch_swiglu(void* X, size_t Xb, void* Wg, size_t Wgb, void* Wu
     void* dg = resolve(Wg, wbytes, 16, true, false);
     void* du = resolve(Wu, wbytes, 16, true, false);
     void* dy = resolve(Out, (size_t)M * Nm * 2, 2, false, true);
-    if (!dx || !dg || !du || !dy) return -5;
+    if (!dx || !dg || !du || !dy) return staging_failed();
     qr::GemmParams p{};
     p.format = format;
     p.X = static_cast<const _Float16*>(dx);
@@ -381,7 +443,7 @@ int m4_bridge_quantize_kv_q8_0(void* src, size_t src_bytes, void* dst, size_t ds
     std::lock_guard<std::mutex> lk(g_mu);
     void* ds = resolve(src, nblocks * 64, 16, true, false);
     void* dd = resolve(dst, nblocks * 34, 2, false, true);
-    if (!ds || !dd) return -5;
+    if (!ds || !dd) return staging_failed();
     hipError_t e = qr::launch_quantize_q8_0(static_cast<const _Float16*>(ds), static_cast<uint8_t*>(dd), nblocks,
                                             g_stream);
     finish_outputs();
@@ -406,7 +468,7 @@ int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t 
     void* dk = resolve(Kq, nk / 32 * 34, 4, true, false);
     void* dv = resolve(Vq, nk / 32 * 34, 4, true, false);
     void* dout = resolve(O, n * 2, 8, false, true);
-    if (!dq || !dk || !dv || !dout) return -5;
+    if (!dq || !dk || !dv || !dout) return staging_failed();
     // Q8_0 -> dequantized fp16 K [Hkv, Mp, D] and V^T [Hkv, D, Mp] once, so the
     // attention kernel stages tiles without decoding them per query tile
     const uint32_t Mp = qr::kv_padded_len(M);
@@ -421,7 +483,7 @@ int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t 
         hipError_t ea = hipMalloc(&g_attn_ws, 2 * half_bytes);
         if (ea != hipSuccess) {
             set_error("hipMalloc(attention cache)", ea);
-            return -5;
+            return staging_failed();
         }
         g_attn_ws_bytes = 2 * half_bytes;
     }
@@ -458,7 +520,7 @@ int m4_bridge_dequantize(void* W, size_t Wb, void* out, size_t outb, int format,
     std::lock_guard<std::mutex> lk(g_mu);
     void* dw = resolve(W, wbytes, 16, true, false);
     void* dout = resolve(out, (size_t)N * K * 2, 16, false, true);
-    if (!dw || !dout) return -5;
+    if (!dw || !dout) return staging_failed();
     hipError_t e = qr::launch_dequant(format, static_cast<const uint8_t*>(dw), static_cast<_Float16*>(dout), K, N,
                                       wbytes / N, g_stream);
     finish_outputs();
@@ -519,7 +581,7 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
         hipError_t e = hipMalloc(&g_ws, need);
         if (e != hipSuccess) {
             set_error("hipMalloc(layer scratch)", e);
-            return -5;
+            return staging_failed();
         }
         g_ws_bytes = need;
     }
@@ -618,7 +680,7 @@ int m4_bridge_rmsnorm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb
     void* dx = resolve(X, (size_t)M * D * 2, 16, true, false);
     void* dw = resolve(W, (size_t)D * 2, 16, true, false);
     void* dy = resolve(Y, (size_t)M * D * 2, 16, false, true);
-    if (!dx || !dw || !dy) return -5;
+    if (!dx || !dw || !dy) return staging_failed();
     hipError_t e = qr::launch_rmsnorm(static_cast<const _Float16*>(dx), static_cast<const _Float16*>(dw),
                                       static_cast<_Float16*>(dy), M, D, eps, norm_type, g_stream);
     finish_outputs();
@@ -638,7 +700,7 @@ int m4_bridge_rope(void* T, size_t Tb, uint32_t H, uint32_t M, uint32_t D, float
     if (Tb < n) return -2;
     std::lock_guard<std::mutex> lk(g_mu);
     void* dt = resolve(T, n, 16, true, true);
-    if (!dt) return -5;
+    if (!dt) return staging_failed();
     hipError_t e = qr::launch_rope(static_cast<_Float16*>(dt), H, M, D, theta, offset, traditional, g_stream);
     finish_outputs();
     if (e != hipSuccess) {

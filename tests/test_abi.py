@@ -200,3 +200,23 @@ def test_c_caller_compiles_and_links(libpath, tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "abi_smoke: ok" in r.stdout
+
+
+def test_extract_buffer_strided_and_offset_views(libpath):
+    """tests/redteam_bridge.py:93-134: a strided view is made contiguous (its own
+    byte size, retained until synchronize); a contiguous row slice keeps its
+    byte offset into the parent buffer."""
+    import torch
+
+    import m4_bridge
+
+    B = m4_bridge.HIPBridge
+    for X in (np.ones((64, 64), np.float16), torch.ones((64, 64), dtype=torch.float16)):
+        strided = X[:, ::2]
+        ptr, nbytes = B.extract_buffer_address_and_size(strided)
+        assert ptr != 0 and nbytes == 64 * 32 * 2
+        base, _ = B.extract_buffer_address_and_size(X)
+        sub, sub_bytes = B.extract_buffer_address_and_size(X[10:20, :])
+        assert sub - base == 10 * 64 * 2 and sub_bytes == 10 * 64 * 2
+    assert len(B._retained_contig) >= 2
+    B._retained_contig.clear()

@@ -174,6 +174,62 @@ def test_router_kernels_by_name(bridge, oracle):
         bridge.dispatch_router_kernel("quant_router_head_gemm_q4_0_64x64", dev(X), W, Y, M, N, K)
 
 
+def test_host_range_into_protected_page_returns_minus_5(bridge):
+    """tests/redteam_bridge.py:178-221: a host X running from a readable page
+    into a PROT_NONE page gives -5 (no fault); the dispatch's staged host
+    output is never written back, and the bridge keeps working."""
+    import ctypes
+    import mmap
+
+    pg = mmap.PAGESIZE
+    buf = mmap.mmap(-1, 2 * pg, mmap.MAP_PRIVATE | mmap.MAP_ANONYMOUS, mmap.PROT_READ | mmap.PROT_WRITE)
+    cobj = ctypes.c_char.from_buffer(buf)
+    base = ctypes.addressof(cobj)
+    libc = ctypes.CDLL(None)
+    libc.mprotect.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert libc.mprotect(base + pg, pg, 0) == 0
+    try:
+        M, K, N = 32, 64, 64
+        assert M * K * 2 <= pg
+        W = np.zeros(K // 32 * N * 18, np.uint8)
+        Y = np.full((M, N), 7.0, np.float16)
+        ret = bridge._lib.m4_bridge_dispatch_gemm(base + 100, M * K * 2, W.ctypes.data, W.nbytes, Y.ctypes.data,
+                                                  Y.nbytes, 0, M, K, N)
+        assert ret == -5
+        bridge.synchronize()
+        assert np.all(Y == 7.0)
+        X = np.zeros((M, K), np.float16)
+        ret = bridge._lib.m4_bridge_dispatch_gemm(X.ctypes.data, X.nbytes, W.ctypes.data, W.nbytes, Y.ctypes.data,
+                                                  Y.nbytes, 0, M, K, N)
+        assert ret == 0
+        bridge.synchronize()
+        assert np.all(Y == 0.0)  # zero scales: every output is 0
+    finally:
+        libc.mprotect(base + pg, pg, 3)
+        del cobj
+        buf.close()
+
+
+def test_in_flight_buffers_retained_until_synchronize(bridge):
+    """tests/redteam_bridge.py:486-528: the bridge holds the tensors of issued
+    work until synchronize(), so dropping the caller's references is safe."""
+    import gc
+
+    import torch
+
+    M, K, N = 512, 512, 512
+    X = torch.ones((M, K), dtype=torch.float16, device="cuda")
+    W = torch.zeros(K // 32 * N * 18, dtype=torch.uint8, device="cuda")
+    Y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    bridge.dispatch_gemm(X, W, Y, 0, M, K, N)
+    before = len(bridge._in_flight_tensors)
+    assert before > 0
+    del X, W, Y
+    gc.collect()
+    bridge.synchronize()
+    assert len(bridge._in_flight_tensors) == 0
+
+
 def test_gemm_q4_0_scales_beyond_fast_path(bridge, oracle):
     """Q4_0 scales with |d| > 8188 (-8 d is not finite in binary16): the tiled
     kernel's fused fma(q, d, -8 d) decode cannot form them, so the wave takes
