@@ -725,6 +725,29 @@ def test_deferred_tripwire_on_device_output(bridge):
     bridge.synchronize()
 
 
+def test_every_format_zero_weights_and_nan_activation(bridge):
+    """tests/redteam_bridge.py:227-272 and :531-580: all six projection formats
+    with all-zero weight blocks run and give a finite (zero) output; an
+    activation NaN injected with zero weights trips the deferred check."""
+    import torch
+
+    M, K, N = 64, 256, 64
+    X = torch.ones((M, K), dtype=torch.float16, device="cuda")
+    for fmt, blk_w, blk_b in [(0, 32, 18), (1, 32, 20), (2, 256, 144), (3, 32, 12), (4, 256, 160), (5, 256, 144)]:
+        W = torch.zeros((K // blk_w) * N * blk_b, dtype=torch.uint8, device="cuda")
+        Y = torch.full((M, N), 3.0, dtype=torch.float16, device="cuda")
+        assert bridge.dispatch_gemm(X, W, Y, fmt, M, K, N, check_finite=True) == 0
+        bridge.synchronize()
+        assert torch.all(Y == 0), fmt
+    Xn = torch.ones((M, K), dtype=torch.float16, device="cuda")
+    Xn[0, 0] = float("nan")
+    W = torch.zeros((K // 32) * N * 18, dtype=torch.uint8, device="cuda")
+    Y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    bridge.dispatch_gemm(Xn, W, Y, 0, M, K, N, check_finite=True)
+    with pytest.raises(FloatingPointError):
+        bridge.synchronize()
+
+
 def test_extension_entry_points_error_codes(bridge):
     """Argument checks of the block-extra entry points, before any device work."""
     lib = bridge.lib
