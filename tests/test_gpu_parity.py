@@ -230,6 +230,27 @@ def test_in_flight_buffers_retained_until_synchronize(bridge):
     assert len(bridge._in_flight_tensors) == 0
 
 
+@pytest.mark.parametrize("fmt,M,K,N", [(1, 128, 4096, 14336), (0, 2048, 2048, 3072), (3, 256, 2048, 5120)])
+def test_under_filled_grid_shapes(bridge, oracle, fmt, M, K, N):
+    """Full-size shapes whose tile grid under-fills the 256 CUs (the headline:
+    112 tiles x 2 K splits; 384 tiles = 1.5 rounds; 80 tiles x 2 splits),
+    checked against the oracle on a row sample (every output column) and for
+    run-to-run determinism of the split-K reduction."""
+    X = synth.activations(M, K, 120 + fmt, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 121 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    rows = np.unique(np.r_[0, 1, 63, 64, 127, np.arange(0, M, 37), M - 1])
+    Xs = np.ascontiguousarray(X[rows])
+    ref = oracle.gemm(fmt, Xs, W, N)
+    tolerance.check(host(Y)[rows], ref, tolerance.gemm_bound(ref, absxw(oracle, fmt, Xs, W, K, N), K))
+    Y2 = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y2, fmt, M, K, N)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(Y2).view(np.uint16), host(Y).view(np.uint16))  # deterministic
+
+
 def test_gemm_q4_0_scales_beyond_fast_path(bridge, oracle):
     """Q4_0 scales with |d| > 8188 (-8 d is not finite in binary16): the tiled
     kernel's fused fma(q, d, -8 d) decode cannot form them, so the wave takes
