@@ -62,62 +62,80 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const _Float16* X, const _
     }
 }
 
-// One thread per (row, 8 consecutive pairs).  Angles are formed in double
+// One thread per (position, 8 consecutive pairs, group of kRopeHeads heads):
+// the angles depend only on the position and the pair, so they are formed
+// once and applied to every head of the group.  Angles are formed in double
 // (pos * theta^(-2i/D), reduced modulo 2 pi) so long positions keep their
-// precision; sin/cos of the reduced angle in fp32.
-__global__ void __launch_bounds__(256) rope_kernel(_Float16* T, uint32_t rows, uint32_t M, uint32_t D, float theta,
+// precision; sin/cos of the reduced angle in fp32.  T is [H, M, D].
+constexpr uint32_t kRopeHeads = 4;
+
+__global__ void __launch_bounds__(128) rope_kernel(_Float16* T, uint32_t H, uint32_t M, uint32_t D, float theta,
                                                    uint32_t offset, int traditional) {
     const uint32_t half = D / 2, per_row = half / 8;
-    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (size_t)rows * per_row) return;
-    const size_t row = t / per_row;
+    const size_t t = (size_t)blockIdx.x * 128 + threadIdx.x;
+    if (t >= (size_t)M * per_row) return;
+    const uint32_t m = (uint32_t)(t / per_row);
     const uint32_t i0 = (uint32_t)(t % per_row) * 8;  // first pair index of this thread
-    const double pos = (double)(offset + (uint32_t)(row % M));
-    _Float16* x = T + row * D;
-    float a[8], b[8];
-    if (traditional) {  // pairs (2i, 2i + 1): 16 consecutive elements
-        const h8_t u = *reinterpret_cast<const h8_t*>(x + 2 * i0);
-        const h8_t v = *reinterpret_cast<const h8_t*>(x + 2 * i0 + 8);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            a[k] = (float)u[2 * k]; b[k] = (float)u[2 * k + 1];
-            a[k + 4] = (float)v[2 * k]; b[k + 4] = (float)v[2 * k + 1];
-        }
-    } else {            // pairs (i, i + D/2)
-        const h8_t u = *reinterpret_cast<const h8_t*>(x + i0);
-        const h8_t v = *reinterpret_cast<const h8_t*>(x + i0 + half);
-#pragma unroll
-        for (int k = 0; k < 8; k++) { a[k] = (float)u[k]; b[k] = (float)v[k]; }
-    }
+    const uint32_t h0 = blockIdx.y * kRopeHeads;
+    const double pos = (double)(offset + m);
     // inverse frequency of pair i0, then successive ratios theta^(-2/D)
     const double l2t = log2((double)theta);
     const double ratio = exp2(-2.0 / (double)D * l2t);
     double f = exp2(-2.0 * (double)i0 / (double)D * l2t);
     const double two_pi = 6.283185307179586476925286766559, inv_two_pi = 0.15915494309189533576888376337251;
-    float ra[8], rb[8];
+    float sn[8], cs[8];
 #pragma unroll
     for (int k = 0; k < 8; k++, f *= ratio) {
         const double ang = pos * f;
         const float red = (float)__builtin_fma(-two_pi, rint(ang * inv_two_pi), ang);
-        const float sn = sinf(red), cs = cosf(red);
-        ra[k] = a[k] * cs - b[k] * sn;
-        rb[k] = a[k] * sn + b[k] * cs;
+        sn[k] = sinf(red);
+        cs[k] = cosf(red);
     }
-    if (traditional) {
-        h8_t u, v;
+    // element offsets of the thread's two 8-element runs within a row
+    const uint32_t o0 = traditional ? 2 * i0 : i0, o1 = traditional ? 2 * i0 + 8 : i0 + half;
+    h8_t u[kRopeHeads], v[kRopeHeads];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            u[2 * k] = (_Float16)ra[k]; u[2 * k + 1] = (_Float16)rb[k];
-            v[2 * k] = (_Float16)ra[k + 4]; v[2 * k + 1] = (_Float16)rb[k + 4];
+    for (uint32_t j = 0; j < kRopeHeads; j++) {  // all loads first
+        if (h0 + j < H) {
+            const _Float16* x = T + ((size_t)(h0 + j) * M + m) * D;
+            u[j] = *reinterpret_cast<const h8_t*>(x + o0);
+            v[j] = *reinterpret_cast<const h8_t*>(x + o1);
         }
-        *reinterpret_cast<h8_t*>(x + 2 * i0) = u;
-        *reinterpret_cast<h8_t*>(x + 2 * i0 + 8) = v;
-    } else {
-        h8_t u, v;
+    }
 #pragma unroll
-        for (int k = 0; k < 8; k++) { u[k] = (_Float16)ra[k]; v[k] = (_Float16)rb[k]; }
-        *reinterpret_cast<h8_t*>(x + i0) = u;
-        *reinterpret_cast<h8_t*>(x + i0 + half) = v;
+    for (uint32_t j = 0; j < kRopeHeads; j++) {
+        if (h0 + j >= H) break;
+        float a[8], b[8];
+        if (traditional) {  // pairs (2i, 2i + 1): 16 consecutive elements
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                a[k] = (float)u[j][2 * k]; b[k] = (float)u[j][2 * k + 1];
+                a[k + 4] = (float)v[j][2 * k]; b[k + 4] = (float)v[j][2 * k + 1];
+            }
+        } else {            // pairs (i, i + D/2)
+#pragma unroll
+            for (int k = 0; k < 8; k++) { a[k] = (float)u[j][k]; b[k] = (float)v[j][k]; }
+        }
+        float ra[8], rb[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            ra[k] = a[k] * cs[k] - b[k] * sn[k];
+            rb[k] = a[k] * sn[k] + b[k] * cs[k];
+        }
+        h8_t uo, vo;
+        if (traditional) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                uo[2 * k] = (_Float16)ra[k]; uo[2 * k + 1] = (_Float16)rb[k];
+                vo[2 * k] = (_Float16)ra[k + 4]; vo[2 * k + 1] = (_Float16)rb[k + 4];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) { uo[k] = (_Float16)ra[k]; vo[k] = (_Float16)rb[k]; }
+        }
+        _Float16* x = T + ((size_t)(h0 + j) * M + m) * D;
+        *reinterpret_cast<h8_t*>(x + o0) = uo;
+        *reinterpret_cast<h8_t*>(x + o1) = vo;
     }
 }
 
@@ -137,9 +155,10 @@ hipError_t launch_rmsnorm(const _Float16* X, const _Float16* w, _Float16* Y, uin
 hipError_t launch_rope(_Float16* T, uint32_t H, uint32_t M, uint32_t D, float theta, uint32_t offset,
                        int traditional, hipStream_t st) {
     if (D % 16) return hipErrorInvalidValue;
-    const size_t threads = (size_t)H * M * (D / 16);
-    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, T, H * M, M, D, theta,
-                       offset, traditional);
+    if (H == 0 || M == 0) return hipSuccess;
+    const size_t threads = (size_t)M * (D / 16);
+    const dim3 grid((unsigned)((threads + 127) / 128), (H + kRopeHeads - 1) / kRopeHeads);
+    hipLaunchKernelGGL(rope_kernel, grid, dim3(128), 0, st, T, H, M, D, theta, offset, traditional);
     return hipGetLastError();
 }
 
