@@ -508,6 +508,7 @@ static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
         switch (rb_pick(F, p.M, p.N, false)) {
             case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);
             case 3: return rb_launch_cfg<F, QR_RB_BIG_K, false>(p, st);
+            case 4: return rb_launch_cfg<F, QR_RB_MID64, false>(p, st);
             default: return rb_launch_cfg<F, QR_RB_MID, false>(p, st);
         }
     }

@@ -12,6 +12,9 @@ namespace qr {
 //                  heavier decode then overlaps the other wave's MFMAs)
 //   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
 //                  of 128 x 256 at the same K split, half the reduction)
+//   4 (M <  1024, last 128-row tile at most half full, cheap-decode formats):
+//                  QR_RB_MID64 (default 2, 1, 4 -> 64 x 128: e.g. M = 129
+//                  computes 192 rows, not 256)
 //   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
 #ifndef QR_RB_BIG
 #define QR_RB_BIG 4, 2, 4
@@ -21,6 +24,9 @@ namespace qr {
 #endif
 #ifndef QR_RB_MID
 #define QR_RB_MID 4, 1, 4
+#endif
+#ifndef QR_RB_MID64
+#define QR_RB_MID64 2, 1, 4
 #endif
 #ifndef QR_RB_DUAL
 #define QR_RB_DUAL 4, 1, 4
@@ -46,13 +52,20 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
         if (QR_RB_MID_FILL && big_tiles < 256) return 1;
         return 0;
     }
-    return 1;
+    // 64-row tiles decode every weight twice as often per MFMA: worth it only
+    // for the formats with a cheap decode (measured at M = 129: Q4_0, MLX and
+    // ternary 6-20% faster, Q4_K 50% slower)
+    const bool cheap = format == QUANT_Q4_0 || format == QUANT_MLX_4BIT || format == QUANT_TERNARY_1_58 ||
+                       format == QUANT_Q8_0 || format == QUANT_PRISM_Q2_0;
+    const uint32_t tail = M % 128;
+    return (cheap && tail != 0 && tail <= 64) ? 4 : 1;
 }
 inline RbShape rb_dims(int s) {
     switch (s) {
         case 0: return {ShapeOf<QR_RB_BIG>::bm, ShapeOf<QR_RB_BIG>::bn};
         case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
         case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
+        case 4: return {ShapeOf<QR_RB_MID64>::bm, ShapeOf<QR_RB_MID64>::bn};
         default: return {ShapeOf<QR_RB_DUAL>::bm, ShapeOf<QR_RB_DUAL>::bn};
     }
 }

@@ -230,23 +230,26 @@ def test_in_flight_buffers_retained_until_synchronize(bridge):
     assert len(bridge._in_flight_tensors) == 0
 
 
-@pytest.mark.parametrize("fmt,M,K,N", [(1, 128, 4096, 14336), (0, 2048, 2048, 3072), (3, 256, 2048, 5120)])
+@pytest.mark.parametrize("fmt,M,K,N", [(1, 128, 4096, 14336), (0, 2048, 2048, 3072), (3, 256, 2048, 5120),
+                                       (0, 129, 4096, 4096), (1, 129, 4096, 4096), (7, 150, 2048, 1536),
+                                       (6, 300, 2048, 1024)])
 def test_under_filled_grid_shapes(bridge, oracle, fmt, M, K, N):
     """Full-size shapes whose tile grid under-fills the 256 CUs (the headline:
-    112 tiles x 2 K splits; 384 tiles = 1.5 rounds; 80 tiles x 2 splits),
-    checked against the oracle on a row sample (every output column) and for
-    run-to-run determinism of the split-K reduction."""
+    112 tiles x 2 K splits; 384 tiles = 1.5 rounds; 80 tiles x 2 splits) and
+    64-row tiles with a K split (M = 129, 150, 300: last 128-row tile at most
+    half full), checked against the oracle on a row sample (every output
+    column) and for run-to-run determinism of the split-K reduction."""
     X = synth.activations(M, K, 120 + fmt, std=0.35)
     W = synth.random_blocks(fmt, N, K, 121 + fmt)
     Y = empty16(M, N)
-    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
     bridge.synchronize()
     rows = np.unique(np.r_[0, 1, 63, 64, 127, np.arange(0, M, 37), M - 1])
     Xs = np.ascontiguousarray(X[rows])
     ref = oracle.gemm(fmt, Xs, W, N)
     tolerance.check(host(Y)[rows], ref, tolerance.gemm_bound(ref, absxw(oracle, fmt, Xs, W, K, N), K))
     Y2 = empty16(M, N)
-    bridge.dispatch_gemm(dev(X), dev(W), Y2, fmt, M, K, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y2, fmt, M, K, N)
     bridge.synchronize()
     np.testing.assert_array_equal(host(Y2).view(np.uint16), host(Y).view(np.uint16))  # deterministic
 
