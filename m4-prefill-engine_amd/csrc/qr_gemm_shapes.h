@@ -54,7 +54,7 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     }
     // 64-row tiles decode every weight twice as often per MFMA: worth it only
     // for the formats with a cheap decode (measured at M = 129: Q4_0, MLX and
-    // ternary 6-20% faster, Q4_K 50% slower)
+    // ternary 6-20% faster, Q4_K 8-9% slower)
     const bool cheap = format == QUANT_Q4_0 || format == QUANT_MLX_4BIT || format == QUANT_TERNARY_1_58 ||
                        format == QUANT_Q8_0 || format == QUANT_PRISM_Q2_0;
     const uint32_t tail = M % 128;
