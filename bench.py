@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="all", help="comma list of config names or 'all'")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-probes", action="store_true", help="skip the on-device HBM / MFMA ceiling probes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
 
@@ -106,6 +107,13 @@ def rotated(t, nbytes_each: int):
     return [t] + [t.clone() for _ in range(n - 1)]
 
 
+def rotated_sets(Ws):
+    """Copies of a layer's weight set so that the sets span > ROTATE_BYTES."""
+    total = sum(w.numel() for w in Ws)
+    n = max(2, min(64, math.ceil(ROTATE_BYTES / max(1, total))))
+    return [Ws] + [[w.clone() for w in Ws] for _ in range(n - 1)]
+
+
 def check(rc: int, what: str):
     if rc != 0:
         raise RuntimeError(f"{what} failed with status {rc}")
@@ -152,17 +160,20 @@ def bench_swiglu(b, timer, M, K, N, seed):
     Wu = torch.from_numpy(synth.quantized_weights(0, N, K, seed + 2)).cuda()
     Out = torch.empty(M, N, dtype=torch.float16, device="cuda")
     lib = b.lib
-    args = (X.data_ptr(), X.numel() * 2, Wg.data_ptr(), Wg.numel(), Wu.data_ptr(), Wu.numel(), Out.data_ptr(),
-            Out.numel() * 2, 0, M, N, K)
+    # gate + up weights rotate over copies spanning > 512 MB (HBM, not MALL)
+    pairs = list(zip(rotated(Wg, 2 * Wg.numel()), rotated(Wu, 2 * Wu.numel())))
+    wb = Wg.numel()
 
     def step(i):
-        check(lib.m4_bridge_dispatch_swiglu(*args), "swiglu")
+        g, u = pairs[i % len(pairs)]
+        check(lib.m4_bridge_dispatch_swiglu(X.data_ptr(), X.numel() * 2, g.data_ptr(), wb, u.data_ptr(), wb,
+                                            Out.data_ptr(), Out.numel() * 2, 0, M, N, K), "swiglu")
 
     ms = timer.run(step)
     flops = 4.0 * M * N * K + 4.0 * M * N  # brick3_swiglu_bench.mm:489
     tf = flops / (ms * 1e-3) / 1e12
     return {"name": "swiglu_q4_0", "M": M, "K": K, "N_mlp": N, "ms": round(ms, 5), "tflops": round(tf, 2),
-            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "timing": timer.mode}
+            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "weight_copies": len(pairs), "timing": timer.mode}
 
 
 def bench_attention(b, timer, H, M, D, seed):
@@ -202,9 +213,10 @@ def bench_layer(b, timer, M, dm, H, D, Nm, seed):
     Ws = [torch.from_numpy(synth.quantized_weights(0, n, k, seed + 1 + i)).cuda() for i, (n, k) in enumerate(shapes)]
     Xo = torch.empty(M, dm, dtype=torch.float16, device="cuda")
     lib = b.lib
-    ptrs = [X.data_ptr()] + [w.data_ptr() for w in Ws] + [Xo.data_ptr()]
+    sets = rotated_sets(Ws)
 
     def step(i):
+        ptrs = [X.data_ptr()] + [w.data_ptr() for w in sets[i % len(sets)]] + [Xo.data_ptr()]
         check(lib.m4_bridge_prefill_layer(*ptrs, 0, M, dm, H, D, Nm, 1.0 / math.sqrt(D)), "layer")
 
     ms = timer.run(step)
@@ -212,7 +224,7 @@ def bench_layer(b, timer, M, dm, H, D, Nm, seed):
     flops = 2.0 * M * dm * HD * 4 + 2.0 * M * dm * Nm * 3 + 2.0 * H * M * (M + 1) * D
     tf = flops / (ms * 1e-3) / 1e12
     return {"name": "layer_llama32_1b_q4_0_q8kv", "M": M, "d_model": dm, "H": H, "D": D, "N_mlp": Nm,
-            "ms": round(ms, 5), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4),
+            "weight_copies": len(sets), "ms": round(ms, 5), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4),
             "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
 
 
@@ -230,10 +242,12 @@ def bench_layer_ex(b, timer, M, dm, Hq, Hkv, D, Nm, seed):
     nf = torch.ones(dm, dtype=torch.float16, device="cuda")
     Xo = torch.empty(M, dm, dtype=torch.float16, device="cuda")
     lib = b.lib
-    ptrs = ([X.data_ptr(), na.data_ptr()] + [w.data_ptr() for w in Ws[:4]] + [nf.data_ptr()] +
-            [w.data_ptr() for w in Ws[4:]] + [Xo.data_ptr()])
+    sets = rotated_sets(Ws)
 
     def step(i):
+        ws = sets[i % len(sets)]
+        ptrs = ([X.data_ptr(), na.data_ptr()] + [w.data_ptr() for w in ws[:4]] + [nf.data_ptr()] +
+                [w.data_ptr() for w in ws[4:]] + [Xo.data_ptr()])
         check(lib.m4_bridge_prefill_layer_ex(*ptrs, 0, M, dm, Hq, Hkv, D, Nm, 1.0 / math.sqrt(D), 1, 1e-5, 1,
                                              500000.0, 0, 0), "layer_ex")
 
@@ -242,7 +256,7 @@ def bench_layer_ex(b, timer, M, dm, Hq, Hkv, D, Nm, seed):
              2.0 * Hq * M * (M + 1) * D)
     tf = flops / (ms * 1e-3) / 1e12
     return {"name": "block_llama32_1b_gqa8_rmsnorm_rope", "M": M, "d_model": dm, "Hq": Hq, "Hkv": Hkv, "D": D,
-            "N_mlp": Nm, "ms": round(ms, 5), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4),
+            "N_mlp": Nm, "weight_copies": len(sets), "ms": round(ms, 5), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4),
             "tokens_per_s": round(M / (ms * 1e-3), 1), "timing": timer.mode}
 
 
@@ -316,18 +330,56 @@ def bench_copy(timer, nbytes: int):
             "gbs": round(2.0 * nbytes / (ms * 1e-3) / 1e9, 1), "timing": timer.mode}
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_rb_mlx_m128_traffic.md"
+# Sources of the headline kernel: a traffic figure measured on other
+# versions of these files is stale and is not reported.
+KERNEL_SOURCES = ("qr_gemm.hip", "qr_gemm_host.hip", "qr_gemm_shapes.h", "qr_decode.h", "qr_device.h",
+                  "qr_formats.h", "qr_kernels.h")
+
+
+def kernel_digest() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        h.update((PKG / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch of the headline kernel, as measured by the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
-    profiles/gemm_rb_mlx_m128_traffic.md (copy-calibrated); None if absent."""
-    path = ROOT / "profiles" / "gemm_rb_mlx_m128_traffic.md"
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in TRAFFIC_PROFILE
+    (copy-calibrated), with the digest of the kernel sources it was measured
+    on.  Returns (bytes or None, note)."""
     try:
-        for line in path.read_text().splitlines():
-            if line.startswith(f"traffic_bytes_per_launch {name}:"):
-                return int(line.split(":")[1])
+        lines = TRAFFIC_PROFILE.read_text().splitlines()
     except OSError:
-        pass
-    return None
+        return None, "no traffic profile"
+    digest = next((ln.split(":", 1)[1].strip() for ln in lines if ln.startswith("kernel_sources_sha256_16:")), None)
+    value = next((int(ln.split(":", 1)[1]) for ln in lines if ln.startswith(f"traffic_bytes_per_launch {name}:")),
+                 None)
+    if value is None:
+        return None, "no traffic figure for " + name
+    now = kernel_digest()
+    if digest != now:
+        return None, f"stale: profile measured on kernel sources {digest}, these are {now}"
+    return value, f"rocprofv3 FETCH_SIZE + WRITE_SIZE, kernel sources {now}"
+
+
+def probes(b):
+    """On-device ceilings (the reference's roofline probes): HBM read and copy
+    GB/s over 1 GiB, dense fp16 MFMA TFLOP/s and the clock it ran at."""
+    import ctypes
+
+    r, c, t, g = (ctypes.c_double() for _ in range(4))
+    out = {}
+    if b.lib.m4_probe_hbm_bandwidth(1 << 30, 5, ctypes.byref(r), ctypes.byref(c)) == 0:
+        out.update(hbm_read_gbs=round(r.value, 1), hbm_copy_gbs=round(c.value, 1),
+                   hbm_read_frac_of_peak=round(r.value / PEAK_HBM_GBS, 4))
+    if b.lib.m4_probe_mfma_f16(4096, 5, ctypes.byref(t), ctypes.byref(g)) == 0:
+        out.update(mfma_f16_tflops=round(t.value, 1), mfma_clock_ghz=round(g.value, 3),
+                   mfma_frac_of_peak=round(t.value / PEAK_MFMA_TFLOPS, 4))
+    return out
 
 
 def cpu_baseline(fmt, X, Wn, N, seconds: float):
@@ -382,9 +434,11 @@ def main():
         per["cfg3_q4_k_m2048"], _ = bench_projection(b, timer, "cfg3_q4_k_m2048", 2, 2048, 4096, 4096, 30)
     if on("cfg4_ternary_m129"):
         per["cfg4_ternary_m129"], _ = bench_projection(b, timer, "cfg4_ternary_m129", 3, 129, 2048, 8192, 40)
+    # every router format at the north-star shape M = 2048, K = 4096 (Q4_K is
+    # cfg3 above); the 3/5-bit formats only when named
     for fmt, tag in ((0, "q4_0"), (1, "mlx"), (3, "ternary"), (4, "var_rate"), (5, "exl3")):
         name = f"m2048_k4096_{tag}"
-        if want is not None and name in want:
+        if (want is None and fmt < 4) or (want is not None and name in want):
             per[name], _ = bench_projection(b, timer, name, fmt, 2048, 4096, 4096, 60 + fmt)
     for name, (M, K, N) in (("ref_fp16_gemm_m128_k4096_n14336", (128, 4096, 14336)),
                             ("ref_fp16_gemm_m2048_k4096_n4096", (2048, 4096, 4096))):
@@ -406,7 +460,8 @@ def main():
         per["rope"] = bench_rope(b, timer, 32, 2048, 64, 55)
 
     head = per.get("cfg2_mlx_m128") or next(iter(per.values()))
-    traffic = traffic_from_profile("cfg2_mlx_m128") if "cfg2_mlx_m128" in per else None
+    traffic, traffic_note = (traffic_from_profile("cfg2_mlx_m128") if "cfg2_mlx_m128" in per
+                             else (None, "headline not run"))
     out = {
         "metric": "ms + effective TFLOPS per quantized projection at M=33/128/2048, K=4096",
         "value": head["tflops"],
@@ -424,9 +479,12 @@ def main():
                    "M": 128, "K": 4096, "N": 14336, "format": "MLX_4BIT (g64 repacked to 32-blocks)"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": traffic,
+                     "traffic_note": traffic_note,
                      "kernel": "gemm_rb_kernel<MLX_4BIT, 4, 1, 4> (128x128 tiles, K split 2)", "hbm_frac": head.get("frac_hbm")},
         "per_config": per,
     }
+    if not a.no_probes:
+        out["probes"] = probes(b)
     if not a.no_cpu_baseline and head_inputs is not None:
         X, Wn = head_inputs
         out["cpu_baseline"] = cpu_baseline(1, X, Wn, 14336, a.cpu_seconds)

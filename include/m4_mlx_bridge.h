@@ -202,6 +202,20 @@ M4_API void* m4_bridge_get_stream(void);
 /* Text of the last device error seen by the bridge ("" if none). */
 M4_API const char* m4_bridge_last_error(void);
 
+/* ---- roofline probes (quant_router_kernels.metal:71-104, timed as in
+ *      bench_universal_router.mm:645-717) ------------------------------- */
+
+/* probe_memory_bandwidth: HBM GB/s of a read-only stream over `bytes` (> the
+ * 256 MB Infinity Cache to measure HBM) and of the reference's dst = src + 1
+ * copy (bytes read + written), best of `reps` timed runs after one warmup.
+ * Allocates its own buffers; runs on the null stream.  0, -2, -4 or -6. */
+M4_API int m4_probe_hbm_bandwidth(size_t bytes, int reps, double* read_gbs, double* copy_gbs);
+/* probe_fma_roofline, on the matrix pipe: dense fp16 TFLOP/s of back-to-back
+ * v_mfma_f32_32x32x16_f16 on every SIMD (`iters` rounds of 4 independent
+ * chains per wave), best of `reps`, and the average shader clock (GHz) the
+ * waves saw (shader-cycle counter over the 100 MHz real-time counter). */
+M4_API int m4_probe_mfma_f16(uint32_t iters, int reps, double* tflops, double* clock_ghz);
+
 /* ---- format registry (src/router/quant_registry.h:14-65) ---------------- */
 
 typedef struct {

@@ -144,12 +144,18 @@ template <bool FROM_Q8>
 __device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t w[16]) {
     uint32_t d16, codes[8];  // code word c: codes of elements 4c .. 4c + 3
     if constexpr (FROM_Q8) {
-        const size_t o = blk * 34;  // 2-byte aligned: nine aligned dwords cover the block
-        const uint32_t* q = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(src) + (o & ~(size_t)3));
+        // 34-byte blocks are 2-byte aligned.  From the aligned dword at or
+        // below the block, eight dwords plus the next two bytes (block at a
+        // dword boundary) or nine dwords (block at 2 mod 4) cover it exactly,
+        // so nothing past the block's last byte is read.
+        const size_t o = blk * 34;
+        const uint8_t* base = static_cast<const uint8_t*>(src) + (o & ~(size_t)3);
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(base);
+        const bool par = (o & 2u) != 0;
         uint32_t raw[9];
 #pragma unroll
-        for (int i = 0; i < 9; i++) raw[i] = q[i];
-        const bool par = (o & 2u) != 0;
+        for (int i = 0; i < 8; i++) raw[i] = q[i];
+        raw[8] = par ? q[8] : (uint32_t)*reinterpret_cast<const uint16_t*>(base + 32);
         d16 = par ? (raw[0] >> 16) : (raw[0] & 0xffffu);
 #pragma unroll
         for (int c = 0; c < 8; c++) codes[c] = par ? raw[c + 1] : __builtin_amdgcn_alignbyte(raw[c + 1], raw[c], 2);

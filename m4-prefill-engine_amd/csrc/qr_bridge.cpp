@@ -51,6 +51,10 @@ void* g_ws = nullptr;
 size_t g_ws_bytes = 0;
 void* g_attn_ws = nullptr;
 size_t g_attn_ws_bytes = 0;
+// Workspaces outgrown by a larger call.  A HIP graph captured earlier may
+// still hold their addresses, so they stay allocated until shutdown.
+std::vector<void*> g_retired;
+size_t g_retired_bytes = 0;
 
 void set_error(const char* where, hipError_t e) {
     char buf[256];
@@ -77,10 +81,23 @@ void* device_view(void* p) {
 // outputs, written) by this process.  The reference wraps host memory with
 // newBufferWithBytesNoCopy and returns -5 when that fails for a range running
 // into an unmapped or protected page (tests/redteam_bridge.py:178-221); here
-// the staging copy would fault instead, so the range is probed first: one byte
-// per page through process_vm_readv / process_vm_writev on this process,
-// which report EFAULT rather than raising a signal.  Where the calls are not
-// permitted at all the probe is skipped.
+// the staging copy would fault instead, so the range is probed first, one
+// byte per page, by system calls that report EFAULT rather than raise a
+// signal: process_vm_readv / process_vm_writev on this process, or where
+// those are not permitted (seccomp), a pipe -- write(2) from the page reads
+// it, read(2) of that byte back into the page writes it unchanged.  When no
+// probe is possible the range counts as inaccessible (fail closed: -5).
+bool page_ok_pipe(int fds[2], const void* q, bool write) {
+    char sink;
+    if (::write(fds[1], q, 1) != 1) return false;  // EFAULT: not readable
+    if (write) {
+        if (::read(fds[0], const_cast<void*>(q), 1) == 1) return true;
+        (void)::read(fds[0], &sink, 1);  // not writable: drain the byte
+        return false;
+    }
+    return ::read(fds[0], &sink, 1) == 1;
+}
+
 bool host_range_ok(const void* p, size_t bytes, bool write) {
     if (bytes == 0) return true;
     const uintptr_t pg = (uintptr_t)sysconf(_SC_PAGESIZE);
@@ -102,13 +119,22 @@ bool host_range_ok(const void* p, size_t bytes, bool write) {
         }
         errno = 0;
         ssize_t got = process_vm_readv(getpid(), loc, n, rem, n, 0);
-        if (got < 0 && errno != EFAULT) return true;  // probe unavailable
-        if (got != n) return false;
-        if (write) {
-            got = process_vm_writev(getpid(), loc, n, rem, n, 0);  // the bytes just read, unchanged
-            if (got < 0 && errno != EFAULT) return true;
+        if (got >= 0 || errno == EFAULT) {
             if (got != n) return false;
+            if (write) {
+                got = process_vm_writev(getpid(), loc, n, rem, n, 0);  // the bytes just read, unchanged
+                if (got != n) return false;
+            }
+            continue;
         }
+        // process_vm_* not permitted: probe this batch's pages through a pipe
+        int fds[2];
+        if (pipe(fds) != 0) return false;
+        bool ok = true;
+        for (int i = 0; i < n && ok; i++) ok = page_ok_pipe(fds, rem[i].iov_base, write);
+        close(fds[0]);
+        close(fds[1]);
+        if (!ok) return false;
     }
     return true;
 }
@@ -117,6 +143,30 @@ bool host_range_ok(const void* p, size_t bytes, bool write) {
 // is device memory aligned to `align`, else a staged copy.  For outputs
 // (`out`), the staged copy is written back at synchronize.  Returns null on
 // allocation/copy failure.
+// Host outputs of earlier dispatches are copied back at synchronize.  A host
+// input that overlaps one of them must see that result (the reference's
+// in-order queue on zero-copy buffers does), so before such an input is
+// staged the stream is drained and every pending host output written back,
+// in dispatch order.
+void flush_pending_host_outputs(const void* p, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = a + bytes;
+    bool overlap = false;
+    for (const auto& st : g_staged) {
+        if (!st.host || !st.armed) continue;
+        const uintptr_t sa = reinterpret_cast<uintptr_t>(st.host), sb = sa + st.bytes;
+        overlap |= sa < b && a < sb;
+    }
+    if (!overlap) return;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) set_error("hipStreamSynchronize", e);
+    for (auto& st : g_staged) {
+        if (!st.host || !st.armed) continue;
+        e = hipMemcpy(st.host, st.dev, st.bytes, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) set_error("hipMemcpy(stage out)", e);
+        st.host = nullptr;
+    }
+}
+
 void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
     void* d = device_view(p);
     if (d && (reinterpret_cast<uintptr_t>(d) % align) == 0) return d;
@@ -124,6 +174,7 @@ void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
         g_last_error = "host buffer range is not accessible";
         return nullptr;
     }
+    if (!d && in) flush_pending_host_outputs(p, bytes);
     void* s = nullptr;
     hipError_t e = hipMalloc(&s, bytes ? bytes : 16);
     if (e != hipSuccess) {
@@ -161,15 +212,24 @@ void finish_outputs() {
     }
 }
 
-// A dispatch whose buffers could not all be staged returns -5 before any
-// launch: the outputs it staged are never copied back.
-int staging_failed() {
+// A dispatch that fails -- buffers that could not all be staged (-5), or a
+// launch error (-6) -- never copies its staged outputs back: the caller's
+// output buffers are left untouched.
+int dispatch_failed(int rc) {
     for (auto& st : g_staged)
         if (!st.armed) {
             st.armed = true;
             st.host = nullptr;
         }
-    return -5;
+    return rc;
+}
+int staging_failed() { return dispatch_failed(-5); }
+
+// Ends a dispatch: outputs armed on success, disarmed on failure.
+int finish(int rc) {
+    if (rc) return dispatch_failed(rc);
+    finish_outputs();
+    return 0;
 }
 
 void sync_and_release() {
@@ -217,31 +277,47 @@ size_t g_sk_ws_floats = 0;
 uint32_t* g_sk_cnt = nullptr;
 size_t g_sk_cnt_n = 0;
 
-hipError_t ensure_skinny_ws(size_t floats, size_t groups) {
-    if (floats > g_sk_ws_floats) {
-        if (g_sk_ws) {
-            (void)hipStreamSynchronize(g_stream);
-            (void)hipFree(g_sk_ws);
-        }
-        g_sk_ws = nullptr;
-        g_sk_ws_floats = 0;
-        hipError_t e = hipMalloc(&g_sk_ws, floats * sizeof(float));
-        if (e != hipSuccess) return e;
-        g_sk_ws_floats = floats;
+// Makes `buf` hold at least `need` bytes.  Growing allocates a new buffer and
+// retires the old one (kept until shutdown: a graph captured before may
+// still launch kernels that use it).  Allocation is not allowed while the
+// stream is being captured: the call must have run once at its size first.
+hipError_t grow(void** buf, size_t* bytes, size_t need, bool zero, const char* what) {
+    if (need <= *bytes) return hipSuccess;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        g_last_error = std::string(what) +
+                       ": workspace must grow while the stream is being captured; run the call once at this size "
+                       "before capturing it";
+        return hipErrorStreamCaptureUnsupported;
     }
-    if (groups > g_sk_cnt_n) {
-        if (g_sk_cnt) {
-            (void)hipStreamSynchronize(g_stream);
-            (void)hipFree(g_sk_cnt);
-        }
-        g_sk_cnt = nullptr;
-        g_sk_cnt_n = 0;
-        hipError_t e = hipMalloc(&g_sk_cnt, groups * sizeof(uint32_t));
-        if (e == hipSuccess) e = hipMemset(g_sk_cnt, 0, groups * sizeof(uint32_t));
-        if (e != hipSuccess) return e;
-        g_sk_cnt_n = groups;
+    void* nb = nullptr;
+    hipError_t e = hipMalloc(&nb, need);
+    if (e == hipSuccess && zero) e = hipMemset(nb, 0, need);
+    if (e != hipSuccess) {
+        if (nb) (void)hipFree(nb);
+        set_error(what, e);
+        return e;
     }
+    if (*buf) {
+        g_retired.push_back(*buf);
+        g_retired_bytes += *bytes;
+    }
+    *buf = nb;
+    *bytes = need;
     return hipSuccess;
+}
+
+hipError_t ensure_skinny_ws(size_t floats, size_t groups) {
+    size_t wb = g_sk_ws_floats * sizeof(float), cb = g_sk_cnt_n * sizeof(uint32_t);
+    void* w = g_sk_ws;
+    void* c = g_sk_cnt;
+    hipError_t e = grow(&w, &wb, floats * sizeof(float), false, "split-K workspace");
+    if (e == hipSuccess) e = grow(&c, &cb, groups * sizeof(uint32_t), true, "split-K counters");
+    g_sk_ws = static_cast<float*>(w);
+    g_sk_ws_floats = wb / sizeof(float);
+    g_sk_cnt = static_cast<uint32_t*>(c);
+    g_sk_cnt_n = cb / sizeof(uint32_t);
+    return e;
 }
 
 int launch(const qr::GemmParams& p0) {
@@ -250,10 +326,7 @@ int launch(const qr::GemmParams& p0) {
         uint32_t ks = 0, groups = 0;
         size_t floats = qr::skinny_workspace_floats(p.M, p.N, p.K, &ks, &groups);
         hipError_t e = ensure_skinny_ws(floats ? floats : 1, groups);
-        if (e != hipSuccess) {
-            set_error("hipMalloc(split-K workspace)", e);
-            return staging_failed();
-        }
+        if (e != hipSuccess) return staging_failed();
         e = qr::launch_gemm_skinny(p, g_sk_ws, g_sk_cnt, g_stream);
         if (e != hipSuccess) {
             set_error("launch_gemm_skinny", e);
@@ -266,10 +339,7 @@ int launch(const qr::GemmParams& p0) {
         uint32_t tiles = 0;
         size_t floats = qr::gemm_workspace_floats(p, p.ksplit, &tiles);
         hipError_t e = ensure_skinny_ws(floats, tiles);
-        if (e != hipSuccess) {
-            set_error("hipMalloc(split-K workspace)", e);
-            return staging_failed();
-        }
+        if (e != hipSuccess) return staging_failed();
         p.ws = g_sk_ws;
         p.counters = g_sk_cnt;
     }
@@ -304,9 +374,7 @@ int gemm_common(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, void
     p.M = M; p.N = N; p.K = K;
     p.head_D = head_D;
     p.col_bytes = wbytes / N;
-    rc = launch(p);
-    finish_outputs();
-    return rc;
+    return finish(launch(p));
 }
 
 }  // namespace
@@ -429,9 +497,7 @@ int m4_bridge_dispatch_swiglu(void* X, size_t Xb, void* Wg, size_t Wgb, void* Wu
     p.Y = static_cast<_Float16*>(dy);
     p.M = M; p.N = Nm; p.K = K;
     p.col_bytes = wbytes / Nm;
-    rc = launch(p);
-    finish_outputs();
-    return rc;
+    return finish(launch(p));
 }
 
 int m4_bridge_quantize_kv_q8_0(void* src, size_t src_bytes, void* dst, size_t dst_bytes, uint64_t nblocks) {
@@ -446,12 +512,8 @@ int m4_bridge_quantize_kv_q8_0(void* src, size_t src_bytes, void* dst, size_t ds
     if (!ds || !dd) return staging_failed();
     hipError_t e = qr::launch_quantize_q8_0(static_cast<const _Float16*>(ds), static_cast<uint8_t*>(dd), nblocks,
                                             g_stream);
-    finish_outputs();
-    if (e != hipSuccess) {
-        set_error("quantize_q8_0", e);
-        return -6;
-    }
-    return 0;
+    if (e != hipSuccess) set_error("quantize_q8_0", e);
+    return finish(e != hipSuccess ? -6 : 0);
 }
 
 int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t Kqb, void* Vq, size_t Vqb, void* O,
@@ -473,32 +535,16 @@ int m4_bridge_dispatch_flash_attn_q8_0_gqa(void* Q, size_t Qb, void* Kq, size_t 
     // attention kernel stages tiles without decoding them per query tile
     const uint32_t Mp = qr::kv_padded_len(M);
     const size_t half_bytes = (size_t)Hkv * Mp * D * 2;
-    if (2 * half_bytes > g_attn_ws_bytes) {
-        if (g_attn_ws) {
-            (void)hipStreamSynchronize(g_stream);
-            (void)hipFree(g_attn_ws);
-            g_attn_ws = nullptr;
-            g_attn_ws_bytes = 0;
-        }
-        hipError_t ea = hipMalloc(&g_attn_ws, 2 * half_bytes);
-        if (ea != hipSuccess) {
-            set_error("hipMalloc(attention cache)", ea);
-            return staging_failed();
-        }
-        g_attn_ws_bytes = 2 * half_bytes;
-    }
+    if (grow(&g_attn_ws, &g_attn_ws_bytes, 2 * half_bytes, false, "attention cache") != hipSuccess)
+        return staging_failed();
     _Float16* kf = static_cast<_Float16*>(g_attn_ws);
     _Float16* vtf = kf + half_bytes / 2;
     hipError_t e = qr::launch_kv_prep(dk, dv, true, kf, vtf, Hkv, M, D, g_stream);
     qr::AttnParams p{static_cast<const _Float16*>(dq), static_cast<_Float16*>(dout), H, M, D, scale,
                      o_token_major ? 1 : 0, Hkv, kf, vtf, Mp};
     if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(p, g_stream);
-    finish_outputs();
-    if (e != hipSuccess) {
-        set_error("flash_attn_q8_0", e);
-        return -6;
-    }
-    return 0;
+    if (e != hipSuccess) set_error("flash_attn_q8_0", e);
+    return finish(e != hipSuccess ? -6 : 0);
 }
 
 int m4_bridge_dispatch_flash_attn_q8_0(void* Q, size_t Qb, void* Kq, size_t Kqb, void* Vq, size_t Vqb, void* O,
@@ -523,12 +569,8 @@ int m4_bridge_dequantize(void* W, size_t Wb, void* out, size_t outb, int format,
     if (!dw || !dout) return staging_failed();
     hipError_t e = qr::launch_dequant(format, static_cast<const uint8_t*>(dw), static_cast<_Float16*>(dout), K, N,
                                       wbytes / N, g_stream);
-    finish_outputs();
-    if (e != hipSuccess) {
-        set_error("dequant", e);
-        return -6;
-    }
-    return 0;
+    if (e != hipSuccess) set_error("dequant", e);
+    return finish(e != hipSuccess ? -6 : 0);
 }
 
 int m4_bridge_prefill_layer(void* X, void* Wq, void* Wk, void* Wv, void* Wo, void* Wg, void* Wu, void* Wd,
@@ -571,20 +613,7 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
     const bool norms = w_attn || w_ffn;
     const size_t need = 2 * al(nq * 2) + 2 * al(nk * 2) + 2 * al(kvf) + al((size_t)M * dm * 2) +
                         al((size_t)M * Nm * 2) + (norms ? al((size_t)M * dm * 2) : 0);
-    if (need > g_ws_bytes) {
-        if (g_ws) {
-            (void)hipStreamSynchronize(g_stream);
-            (void)hipFree(g_ws);
-            g_ws = nullptr;
-            g_ws_bytes = 0;
-        }
-        hipError_t e = hipMalloc(&g_ws, need);
-        if (e != hipSuccess) {
-            set_error("hipMalloc(layer scratch)", e);
-            return staging_failed();
-        }
-        g_ws_bytes = need;
-    }
+    if (grow(&g_ws, &g_ws_bytes, need, false, "layer scratch") != hipSuccess) return -5;
     uint8_t* w = static_cast<uint8_t*>(g_ws);
     auto take = [&](size_t b) { uint8_t* r = w; w += al(b); return r; };
     _Float16* q = reinterpret_cast<_Float16*>(take(nq * 2));
@@ -683,12 +712,8 @@ int m4_bridge_rmsnorm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb
     if (!dx || !dw || !dy) return staging_failed();
     hipError_t e = qr::launch_rmsnorm(static_cast<const _Float16*>(dx), static_cast<const _Float16*>(dw),
                                       static_cast<_Float16*>(dy), M, D, eps, norm_type, g_stream);
-    finish_outputs();
-    if (e != hipSuccess) {
-        set_error("rmsnorm", e);
-        return -6;
-    }
-    return 0;
+    if (e != hipSuccess) set_error("rmsnorm", e);
+    return finish(e != hipSuccess ? -6 : 0);
 }
 
 int m4_bridge_rope(void* T, size_t Tb, uint32_t H, uint32_t M, uint32_t D, float theta, uint32_t offset,
@@ -702,12 +727,8 @@ int m4_bridge_rope(void* T, size_t Tb, uint32_t H, uint32_t M, uint32_t D, float
     void* dt = resolve(T, n, 16, true, true);
     if (!dt) return staging_failed();
     hipError_t e = qr::launch_rope(static_cast<_Float16*>(dt), H, M, D, theta, offset, traditional, g_stream);
-    finish_outputs();
-    if (e != hipSuccess) {
-        set_error("rope", e);
-        return -6;
-    }
-    return 0;
+    if (e != hipSuccess) set_error("rope", e);
+    return finish(e != hipSuccess ? -6 : 0);
 }
 
 void m4_bridge_synchronize(void) {
@@ -723,7 +744,8 @@ double m4_bridge_get_uma_footprint_mb(void) {
         fclose(f);
     }
     double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
-    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 + g_sk_cnt_n * 4) /
+    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 + g_sk_cnt_n * 4 +
+                              g_retired_bytes) /
                          (1024.0 * 1024.0);
 }
 
@@ -744,6 +766,9 @@ void m4_bridge_shutdown(void) {
     g_attn_ws_bytes = 0;
     if (g_sk_ws) (void)hipFree(g_sk_ws);
     if (g_sk_cnt) (void)hipFree(g_sk_cnt);
+    for (void* r : g_retired) (void)hipFree(r);
+    g_retired.clear();
+    g_retired_bytes = 0;
     g_sk_ws = nullptr;
     g_sk_cnt = nullptr;
     g_sk_ws_floats = g_sk_cnt_n = 0;

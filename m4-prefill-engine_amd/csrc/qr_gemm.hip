@@ -312,8 +312,9 @@ gemm_rb_kernel(GemmParams p) {
     // Workspace slot of (split z, tile): ACC / 2 float pairs per thread, pair q
     // of thread t at q * NT + t (coalesced across lanes).  Partials cross XCDs,
     // whose L2s are not coherent with each other: they are written and read
-    // with 64-bit agent-scope atomics (write-through / read-from-memory); the
-    // reads are issued in batches of up to 32 so their latencies overlap.
+    // with 64-bit agent-scope atomics, published by a release / acquire pair
+    // around the tile counter; the reads are issued in batches of up to 32 so
+    // their latencies overlap.
     if (SPLIT && ksplit > 1) {
         constexpr int NP = C::ACC / 2;                 // float pairs per thread
         constexpr int BATCH = NP < 32 ? NP : 32;       // pairs in flight per batch
@@ -339,16 +340,21 @@ gemm_rb_kernel(GemmParams p) {
                             __hip_atomic_store(dst + q * NT, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
         }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
+        // Publication: every thread's partial stores are released at agent
+        // scope before the workgroup barrier; thread 0's counter increment is
+        // an agent-scope acq_rel RMW, so the last arriver's acquire fence
+        // below makes every split's partials visible to all its threads.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         __shared__ uint32_t s_last;
         if (tid == 0) {
             const uint32_t prev =
-                __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             s_last = (prev == ksplit - 1) ? 1u : 0u;
         }
         __syncthreads();
         if (!s_last) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         // sum all splits in split order (deterministic); this workgroup's own
         // split comes from its registers, the others from the workspace
         f16v_t tot[TM][NCB];
@@ -388,6 +394,8 @@ gemm_rb_kernel(GemmParams p) {
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < NCB; j++) acc[i][j] = tot[i][j];
+        // every split has arrived: no other workgroup touches this counter
+        // until the next launch, which the stream orders after this one
         if (tid == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 

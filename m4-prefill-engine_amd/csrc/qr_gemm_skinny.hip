@@ -162,17 +162,6 @@ template <> struct Frag<QUANT_TERNARY_1_58> {
     }
 };
 
-#ifdef QR_SK_TRACE
-__device__ unsigned long long qr_sk_trace[65536];
-#define SK_TRACE(k)                                                                             \
-    do {                                                                                       \
-        if (threadIdx.x == 0)                                                                  \
-            qr_sk_trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + (k)] =               \
-                __builtin_amdgcn_s_memrealtime();                                              \
-    } while (0)
-#else
-#define SK_TRACE(k) ((void)0)
-#endif
 
 constexpr int kSkWaves = 8;
 constexpr int kSkNT = 4;                  // 16-column tiles per wave
@@ -226,7 +215,6 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
     uint8_t* xs = smem;
     uint8_t* wsb = smem + L.x_bytes;
 
-    SK_TRACE(0);
     // ---- load phase: strips and rows to LDS, all loads in flight ----
     {
         auto wr = make_rsrc(p.W + (size_t)n0 * col_bytes, ncols * col_bytes);
@@ -263,7 +251,6 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
         }
     }
     __syncthreads();
-    SK_TRACE(1);
 
     // ---- compute phase: acc[t][mt] rows n = 16t + 4g + i, column m = 16mt + r16 ----
     f4_t acc[kSkNT][MT];
@@ -306,7 +293,6 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
                                                                    acc[t][mt], 0, 0, 0);
         }
     }
-    SK_TRACE(2);
 
     // ---- reduce the 8 waves through LDS (fixed order) ----
     // Per-wave buffer [m][n] with row stride RS = 64 + 4 floats: a lane's four
@@ -358,7 +344,6 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
         }
     };
 
-    SK_TRACE(3);
     if (!split) {
 #pragma unroll
         for (int e = 0; e < PER; e++) emit(tid + 512 * e, tot[e]);
@@ -367,24 +352,24 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
 
     // ---- cross-workgroup split-K: partial slot ks, last arriver sums ----
     // Partials are written with agent-scope atomic stores (coherent across
-    // XCDs without dirtying L2), so publishing them needs only the completion
-    // wait before the counter update -- no L2 writeback or invalidate, which
-    // would evict the operands every other workgroup on the XCD re-reads.
+    // XCDs) and published by a release / acquire pair around the column
+    // group's counter.
     float* slot = ws + ((size_t)ks * gridDim.x + cg) * NEL;
 #pragma unroll
     for (int e = 0; e < PER; e++)
         if (tid + 512 * e < NEL)
             __hip_atomic_store(slot + tid + 512 * e, tot[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores performed
+    // release the partials (agent scope) before the barrier; the counter RMW
+    // is acq_rel and the last arriver acquires before reading the others'
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
-    SK_TRACE(4);
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(counters + cg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = __hip_atomic_fetch_add(counters + cg, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (prev == ksplit - 1) ? 1u : 0u;
     }
     __syncthreads();
-    SK_TRACE(5);
     if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // Sum the split partials in split order; four splits' loads are issued
     // together (indices clamped, not branched) so their latencies overlap.
     static_assert(NEL % 512 == 0, "whole rows of outputs per thread");
@@ -409,7 +394,6 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
 #pragma unroll
     for (int e = 0; e < PER; e++) emit(tid + 512 * e, sum[e]);
     if (tid == 0) __hip_atomic_store(counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    SK_TRACE(6);
 }
 
 static uint32_t group_bytes_rt(int f) {

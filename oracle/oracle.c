@@ -541,6 +541,54 @@ EXPORT int orc_attention_gqa(const uint16_t* Q, const uint16_t* K, const uint16_
     return 0;
 }
 
+/* Row-sampled causal attention: the outputs of query positions pos[0..nr)
+ * only, each computed exactly as attn_head_row computes that row (the output
+ * of query i depends on keys/values 0..i alone, brick4_attn_bench.mm:70-119).
+ * Qr [H, nr, D] holds the sampled queries; K, V [Hkv, M, D]; Or [H, nr, D] or
+ * token-major [nr, H*D].  Used to check full-size shapes on a row sample. */
+typedef struct {
+    const uint16_t* Q; const uint16_t* K; const uint16_t* V; uint16_t* O;
+    const uint32_t* pos; uint32_t nr, H, Hkv, M, D; double scale; int o_token_major;
+} attn_rows_ctx;
+
+static void attn_rows_row(void* vctx, size_t idx) {
+    attn_rows_ctx* c = (attn_rows_ctx*)vctx;
+    size_t h = idx / c->nr, r = idx % c->nr, i = c->pos[r];
+    size_t MD = (size_t)c->M * c->D;
+    size_t hk = h / (c->H / c->Hkv);
+    const uint16_t* q = c->Q + (h * c->nr + r) * c->D;
+    double* s = (double*)malloc(sizeof(double) * (i + 1));
+    double mx = -1e30;
+    for (size_t j = 0; j <= i; j++) {
+        const uint16_t* k = c->K + hk * MD + j * c->D;
+        double dot = 0.0;
+        for (uint32_t d = 0; d < c->D; d++) dot += orc_f16_to_f64(q[d]) * orc_f16_to_f64(k[d]);
+        s[j] = dot * c->scale;
+        if (s[j] > mx) mx = s[j];
+    }
+    double sum = 0.0;
+    for (size_t j = 0; j <= i; j++) { s[j] = exp(s[j] - mx); sum += s[j]; }
+    double inv = (sum > 0.0) ? 1.0 / sum : 0.0;
+    for (uint32_t d = 0; d < c->D; d++) {
+        double acc = 0.0;
+        for (size_t j = 0; j <= i; j++) acc += (s[j] * inv) * orc_f16_to_f64(c->V[hk * MD + j * c->D + d]);
+        size_t o = c->o_token_major ? (r * (size_t)c->H + h) * c->D + d : (h * c->nr + r) * c->D + d;
+        c->O[o] = orc_f64_to_f16(acc);
+    }
+    free(s);
+}
+
+EXPORT int orc_attention_rows(const uint16_t* Qr, const uint16_t* K, const uint16_t* V, uint16_t* Or,
+                              const uint32_t* pos, uint32_t nr, uint32_t H, uint32_t Hkv, uint32_t M,
+                              uint32_t D, float scale, int o_token_major, int nthreads) {
+    if (!Hkv || H % Hkv) return -4;
+    for (uint32_t r = 0; r < nr; r++)
+        if (pos[r] >= M) return -4;
+    attn_rows_ctx c = {Qr, K, V, Or, pos, nr, H, Hkv, M, D, (double)scale, o_token_major};
+    parallel_rows(attn_rows_row, &c, (size_t)H * nr, nthreads);
+    return 0;
+}
+
 /* Attention over a Q8_0 KV cache: the reference checks its Q8_0 kernel
  * against the double gold run on the DEQUANTIZED K/V
  * (brick4_attn_bench.mm:241-255).  Kq/Vq are Q8_0 blocks over [H, M, D]. */
@@ -739,5 +787,73 @@ EXPORT int orc_layer_ex(int f, const uint16_t* X, const uint16_t* w_attn, const 
     rc |= orc_swiglu(f, a, Wg, Wu, s, M, Nm, dm, nthreads);
     rc |= orc_gemm(f, s, Wd, Xout, xm, M, dm, Nm, 0, 0, 0, nthreads);
     free(xn); free(q); free(k); free(v); free(o); free(xm); free(s); free(kq); free(vq);
+    return rc;
+}
+
+/*
+ * orc_layer_ex on a row sample: Xout rows pos[0..nr) only.  Row m of the
+ * layer depends on row m of X and on the K / V of rows 0..m, so K and V are
+ * projected (and Q8_0-quantized) for every row while Q, attention, the
+ * O-projection, the norms and the MLP run on the sampled rows alone -- the
+ * same arithmetic, row by row, as orc_layer_ex.  Xout [nr, dm].
+ */
+EXPORT int orc_layer_ex_rows(int f, const uint16_t* X, const uint16_t* w_attn, const uint8_t* Wq,
+                             const uint8_t* Wk, const uint8_t* Wv, const uint8_t* Wo, const uint16_t* w_ffn,
+                             const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd, uint16_t* Xout,
+                             const uint32_t* pos, uint32_t nr, uint32_t M, uint32_t dm, uint32_t Hq,
+                             uint32_t Hkv, uint32_t D, uint32_t Nm, float scale, int norm_type, float eps,
+                             int rope, float theta, uint32_t offset, int traditional, int nthreads) {
+    if (!Hkv || Hq % Hkv) return -4;
+    for (uint32_t r = 0; r < nr; r++)
+        if (pos[r] >= M) return -4;
+    uint32_t HQ = Hq * D, HK = Hkv * D;
+    size_t nk = (size_t)M * HK;
+    uint16_t* xn = (uint16_t*)malloc((size_t)M * dm * 2);
+    uint16_t* k = (uint16_t*)malloc(nk * 2);
+    uint16_t* v = (uint16_t*)malloc(nk * 2);
+    uint8_t* kq = (uint8_t*)malloc(nk / 32 * 34);
+    uint8_t* vq = (uint8_t*)malloc(nk / 32 * 34);
+    uint16_t* xr = (uint16_t*)malloc((size_t)nr * dm * 2);    /* sampled (normed) rows */
+    uint16_t* x0 = (uint16_t*)malloc((size_t)nr * dm * 2);    /* sampled input rows */
+    uint16_t* q = (uint16_t*)malloc((size_t)nr * HQ * 2);
+    uint16_t* o = (uint16_t*)malloc((size_t)nr * HQ * 2);
+    uint16_t* xm = (uint16_t*)malloc((size_t)nr * dm * 2);
+    uint16_t* xn2 = (uint16_t*)malloc((size_t)nr * dm * 2);
+    uint16_t* s = (uint16_t*)malloc((size_t)nr * Nm * 2);
+    int rc = 0;
+    const uint16_t* a = X;
+    if (w_attn) {
+        rc |= orc_rmsnorm(X, w_attn, xn, M, dm, eps, norm_type);
+        a = xn;
+    }
+    for (uint32_t r = 0; r < nr; r++) {
+        memcpy(xr + (size_t)r * dm, a + (size_t)pos[r] * dm, (size_t)dm * 2);
+        memcpy(x0 + (size_t)r * dm, X + (size_t)pos[r] * dm, (size_t)dm * 2);
+    }
+    rc |= orc_gemm(f, a, Wk, k, NULL, M, HK, dm, 1, Hkv, D, nthreads);
+    rc |= orc_gemm(f, a, Wv, v, NULL, M, HK, dm, 1, Hkv, D, nthreads);
+    rc |= orc_gemm(f, xr, Wq, q, NULL, nr, HQ, dm, 1, Hq, D, nthreads);   /* [Hq, nr, D] */
+    if (rope) {
+        /* the sampled query rows rotate at their own positions */
+        for (uint32_t r = 0; r < nr; r++)
+            for (uint32_t h = 0; h < Hq; h++)
+                rc |= orc_rope(q + ((size_t)h * nr + r) * D, 1, 1, D, theta, offset + pos[r], traditional);
+        rc |= orc_rope(k, Hkv, M, D, theta, offset, traditional);
+    }
+    orc_quantize_q8_0(k, kq, nk / 32);
+    orc_quantize_q8_0(v, vq, nk / 32);
+    orc_dequantize_q8_0(kq, k, nk / 32);
+    orc_dequantize_q8_0(vq, v, nk / 32);
+    rc |= orc_attention_rows(q, k, v, o, pos, nr, Hq, Hkv, M, D, scale, 1, nthreads);
+    rc |= orc_gemm(f, o, Wo, xm, x0, nr, dm, HQ, 0, 0, 0, nthreads);
+    a = xm;
+    if (w_ffn) {
+        rc |= orc_rmsnorm(xm, w_ffn, xn2, nr, dm, eps, norm_type);
+        a = xn2;
+    }
+    rc |= orc_swiglu(f, a, Wg, Wu, s, nr, Nm, dm, nthreads);
+    rc |= orc_gemm(f, s, Wd, Xout, xm, nr, dm, Nm, 0, 0, 0, nthreads);
+    free(xn); free(k); free(v); free(kq); free(vq); free(xr); free(x0); free(q); free(o);
+    free(xm); free(xn2); free(s);
     return rc;
 }

@@ -61,6 +61,10 @@ def lib() -> ctypes.CDLL:
         L.orc_rope.restype = i
         L.orc_layer_ex.argtypes = [i] + [vp] * 11 + [u32] * 6 + [f, i, f, i, f, u32, i, i]
         L.orc_layer_ex.restype = i
+        L.orc_attention_rows.argtypes = [vp] * 5 + [u32] * 5 + [f, i, i]
+        L.orc_attention_rows.restype = i
+        L.orc_layer_ex_rows.argtypes = [i] + [vp] * 12 + [u32] * 7 + [f, i, f, i, f, u32, i, i]
+        L.orc_layer_ex_rows.restype = i
         _lib = L
     return _lib
 
@@ -246,5 +250,45 @@ def layer_ex(fmt: int, X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, Hq: int, Hk
                             _p(nf) if nf is not None else None, *[_p(w) for w in Ws[4:]], _p(out), M, dm, Hq, Hkv,
                             D, N_mlp, scale, norm_type, eps, int(rope), theta, offset, int(traditional),
                             nthreads or threads())
+    assert rc == 0, rc
+    return out
+
+
+def attention_q8_0_rows(Qr, Kq, Vq, pos, M: int, Hkv: int, scale: float, o_token_major: bool = False,
+                        nthreads: int | None = None) -> np.ndarray:
+    """Causal attention over the dequantized Q8_0 K/V [Hkv, M, D] for the query
+    positions `pos` only.  Qr [H, len(pos), D] holds those queries; the result
+    is [H, len(pos), D] (or [len(pos), H*D] token-major)."""
+    Qr = np.ascontiguousarray(Qr, dtype=np.float16)
+    H, nr, D = Qr.shape
+    pos = np.ascontiguousarray(pos, dtype=np.uint32)
+    assert pos.size == nr
+    Kd = dequantize_q8_0(Kq)
+    Vd = dequantize_q8_0(Vq)
+    assert Kd.size == Hkv * M * D
+    out = np.empty((nr, H * D) if o_token_major else (H, nr, D), np.float16)
+    rc = lib().orc_attention_rows(_p(Qr), _p(Kd), _p(Vd), _p(out), _p(pos), nr, H, Hkv, M, D, scale,
+                                  int(o_token_major), nthreads or threads())
+    assert rc == 0, rc
+    return out
+
+
+def layer_ex_rows(fmt: int, X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, pos, Hq: int, Hkv: int, D: int,
+                  N_mlp: int, scale: float, norm_type: int = 1, eps: float = 1e-5, rope: bool = False,
+                  theta: float = 10000.0, offset: int = 0, traditional: bool = False,
+                  nthreads: int | None = None) -> np.ndarray:
+    """Rows `pos` of layer_ex (the plain router layer when w_attn = w_ffn = None,
+    rope = False and Hkv = Hq): [len(pos), d_model]."""
+    X = np.ascontiguousarray(X, dtype=np.float16)
+    M, dm = X.shape
+    pos = np.ascontiguousarray(pos, dtype=np.uint32)
+    na = None if w_attn is None else np.ascontiguousarray(w_attn, dtype=np.float16)
+    nf = None if w_ffn is None else np.ascontiguousarray(w_ffn, dtype=np.float16)
+    Ws = [np.ascontiguousarray(w, dtype=np.uint8) for w in (Wq, Wk, Wv, Wo, Wg, Wu, Wd)]
+    out = np.empty((pos.size, dm), np.float16)
+    rc = lib().orc_layer_ex_rows(fmt, _p(X), _p(na) if na is not None else None, *[_p(w) for w in Ws[:4]],
+                                 _p(nf) if nf is not None else None, *[_p(w) for w in Ws[4:]], _p(out), _p(pos),
+                                 pos.size, M, dm, Hq, Hkv, D, N_mlp, scale, norm_type, eps, int(rope), theta,
+                                 offset, int(traditional), nthreads or threads())
     assert rc == 0, rc
     return out

@@ -1,0 +1,179 @@
+"""GPU parity at the full BASELINE configuration sizes.
+
+Each test runs one BASELINE configuration at its full shape through the
+C-ABI and checks it against the oracle.  Where the oracle would take minutes
+for the whole output, it runs on a row sample of at least 64 rows (every
+column; for attention every head) -- each output row depends only on its own
+activation row (and, for attention and the layer, on the keys/values of
+earlier rows, which the row-sampled oracle still computes in full), so the
+sampled rows are checked exactly as a full run would check them.  The
+reference verifies each of its bench shapes against its gold the same way
+(bench_universal_router.mm:955; brick4_attn_bench.mm:250-255, 320;
+unified_prefill_engine.mm:702).
+
+Bars: flat max |diff| <= 1/128 for the projections, SwiGLU and attention
+(tolerance.check_ref: one fp16 step where |gold| >= 8); 2/128 for the layer,
+whose fp16 intermediates can flip one step upstream (the reference's own
+layer check allows 0.05, unified_prefill_engine.mm:692).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import synth
+import tolerance
+from tolerance import TOL
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def empty16(*shape):
+    import torch
+
+    return torch.empty(*shape, dtype=torch.float16, device="cuda")
+
+
+def sample_rows(M: int, n: int = 64) -> np.ndarray:
+    """>= n rows: both ends, tile edges (32/64/128/256-row tiles) and an even spread."""
+    edges = [0, 1, 31, 32, 63, 64, 127, 128, 129, 255, 256, M // 2, M - 2, M - 1]
+    spread = np.linspace(0, M - 1, n).astype(np.int64)
+    return np.unique(np.clip(np.r_[edges, spread], 0, M - 1))
+
+
+def run_projection(bridge, oracle, fmt, M, K, N, W, seed, rows=None):
+    X = synth.activations(M, K, seed)
+    Y = empty16(M, N)
+    print(f"projection fmt={fmt} M={M} K={K} N={N}", flush=True)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    rows = np.arange(M) if rows is None else rows
+    ref = oracle.gemm(fmt, np.ascontiguousarray(X[rows]), W, N)
+    tolerance.check_ref(host(Y)[rows], ref, what=f"fmt {fmt} {M}x{K}x{N} ({rows.size} rows)")
+    return X, Y
+
+
+def test_cfg2_headline_mlx_m128_k4096_n14336(bridge, oracle):
+    """BASELINE configs[1] (the headline): MLX g64 affine weights from N(0, 0.02)."""
+    M, K, N = 128, 4096, 14336
+    W = synth.quantized_weights(1, N, K, 21)
+    run_projection(bridge, oracle, 1, M, K, N, W, 20, rows=sample_rows(M))
+
+
+def test_cfg3_q4_k_m2048_k4096_n4096(bridge, oracle):
+    """Q4_K from N(0, 0.02), M = 2048 (the 128 x 256
+    eight-wave tile at its full grid)."""
+    M, K, N = 2048, 4096, 4096
+    W = synth.quantized_weights(2, N, K, 31)
+    run_projection(bridge, oracle, 2, M, K, N, W, 30, rows=sample_rows(M))
+
+
+def test_cfg4_ternary_m129_k2048_n8192(bridge, oracle):
+    """ternary {-1, 0, 1} with p = {.25, .5, .25} and one
+    per-tensor scale, M = 129 (not a multiple of the tile), every row."""
+    M, K, N = 129, 2048, 8192
+    W = synth.quantized_weights(3, N, K, 41)
+    run_projection(bridge, oracle, 3, M, K, N, W, 40)
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 3])
+def test_every_format_m2048_k4096(bridge, oracle, fmt):
+    """The remaining router formats at the north-star shape M = 2048, K = 4096."""
+    M, K, N = 2048, 4096, 4096
+    W = synth.quantized_weights(fmt, N, K, 61 + fmt)
+    run_projection(bridge, oracle, fmt, M, K, N, W, 60 + fmt, rows=sample_rows(M))
+
+
+def test_cfg5_swiglu_m2048_k2048_n8192(bridge, oracle):
+    """BASELINE configs[4] MLP: silu(X Wg^T) * (X Wu^T), Q4_0, M = 2048,
+    d_model = 2048, hidden 8192."""
+    M, K, N = 2048, 2048, 8192
+    X = synth.activations(M, K, 50)
+    Wg, Wu = synth.quantized_weights(0, N, K, 51), synth.quantized_weights(0, N, K, 52)
+    out = empty16(M, N)
+    print(f"swiglu M={M} K={K} N={N}", flush=True)
+    bridge.dispatch_swiglu(dev(X), dev(Wg), dev(Wu), out, 0, M, N, K)
+    bridge.synchronize()
+    rows = sample_rows(M)
+    ref = oracle.swiglu(0, np.ascontiguousarray(X[rows]), Wg, Wu, N)
+    tolerance.check_ref(host(out)[rows], ref, what=f"swiglu ({rows.size} rows)")
+
+
+def test_cfg5_attention_h32_m2048_d64(bridge, oracle):
+    """BASELINE configs[4] attention: causal, H = 32, M = 2048, D = 64, Q8_0
+    K/V cache, N(0, 1) inputs, scale 1/8; every head on sampled query rows."""
+    H, M, D = 32, 2048, 64
+    rng = np.random.default_rng(55)
+    Q, K, V = (rng.standard_normal((H, M, D), dtype=np.float32).astype(np.float16) for _ in range(3))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    scale = 1.0 / math.sqrt(D)
+    O = empty16(H, M, D)
+    print(f"attention H={H} M={M} D={D}", flush=True)
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), O, H, M, D, scale)
+    bridge.synchronize()
+    rows = sample_rows(M)
+    ref = oracle.attention_q8_0_rows(np.ascontiguousarray(Q[:, rows]), Kq, Vq, rows, M, H, scale)
+    d = float(np.max(np.abs(host(O)[:, rows].astype(np.float64) - ref.astype(np.float64))))
+    print(f"attention max|diff| {d:.4g} over {H} heads x {rows.size} rows", flush=True)
+    assert d <= TOL
+
+
+def _layer_weights(M, dm, Hq, Hkv, D, Nm, seed):
+    shapes = [(Hq * D, dm), (Hkv * D, dm), (Hkv * D, dm), (dm, Hq * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    return [synth.quantized_weights(0, n, k, seed + 1 + i) for i, (n, k) in enumerate(shapes)]
+
+
+def test_cfg5_layer_m2048(bridge, oracle):
+    """the Llama-3.2-1B-shaped router layer (no norms, no
+    RoPE, as unified_prefill_engine.mm:72-223 composes it), Q4_0 weights,
+    Q8_0 KV, M = 2048, d_model = 2048, H = 32, D = 64, hidden 8192."""
+    M, dm, H, D, Nm = 2048, 2048, 32, 64, 8192
+    X = synth.activations(M, dm, 52)
+    Ws = _layer_weights(M, dm, H, H, D, Nm, 52)
+    out = empty16(M, dm)
+    print(f"layer M={M} d={dm} H={H} D={D} Nm={Nm}", flush=True)
+    bridge.prefill_layer(dev(X), *[dev(w) for w in Ws], out, 0, M, dm, H, D, Nm, 1.0 / math.sqrt(D))
+    bridge.synchronize()
+    rows = sample_rows(M)
+    ref = oracle.layer_ex_rows(0, X, None, *Ws[:4], None, *Ws[4:], rows, Hq=H, Hkv=H, D=D, N_mlp=Nm,
+                               scale=1.0 / math.sqrt(D), rope=False)
+    g = host(out)[rows].astype(np.float64)
+    d = np.abs(g - ref.astype(np.float64))
+    print(f"layer max|diff| {d.max():.4g}; {int((d > TOL).sum())} of {d.size} above 1/128", flush=True)
+    assert np.all(np.isfinite(g)) and d.max() <= 2 * TOL
+
+
+def test_cfg5_full_block_gqa_rmsnorm_rope_m2048(bridge, oracle):
+    """The full Llama-3.2-1B block the bench also times: RMSNorm, RoPE
+    (theta 5e5), grouped-query attention with Hkv = 8, Q4_0 weights, Q8_0 KV."""
+    M, dm, Hq, Hkv, D, Nm = 2048, 2048, 32, 8, 64, 8192
+    X = synth.activations(M, dm, 53)
+    Ws = _layer_weights(M, dm, Hq, Hkv, D, Nm, 53)
+    rng = np.random.default_rng(54)
+    na = (1.0 + 0.1 * rng.standard_normal(dm)).astype(np.float16)
+    nf = (1.0 + 0.1 * rng.standard_normal(dm)).astype(np.float16)
+    out = empty16(M, dm)
+    print(f"block M={M} Hq={Hq} Hkv={Hkv}", flush=True)
+    bridge.prefill_layer_ex(dev(X), dev(na), *[dev(w) for w in Ws[:4]], dev(nf), *[dev(w) for w in Ws[4:]], out,
+                            0, M, dm, Hq, Hkv, D, Nm, 1.0 / math.sqrt(D), norm_type=1, norm_eps=1e-5, rope=True,
+                            rope_theta=500000.0)
+    bridge.synchronize()
+    rows = sample_rows(M)
+    ref = oracle.layer_ex_rows(0, X, na, *Ws[:4], nf, *Ws[4:], rows, Hq=Hq, Hkv=Hkv, D=D, N_mlp=Nm,
+                               scale=1.0 / math.sqrt(D), norm_type=1, eps=1e-5, rope=True, theta=500000.0)
+    g = host(out)[rows].astype(np.float64)
+    d = np.abs(g - ref.astype(np.float64))
+    print(f"block max|diff| {d.max():.4g}; {int((d > TOL).sum())} of {d.size} above 1/128", flush=True)
+    assert np.all(np.isfinite(g)) and d.max() <= 2 * TOL

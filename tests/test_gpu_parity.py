@@ -124,13 +124,9 @@ def test_gemm_var_rate_and_exl3(bridge, oracle, fmt, M, K, N):
     Yh = empty16(H, M, D)
     bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
     bridge.synchronize()
-    axw = absxw(oracle, fmt, X, W, K, N)
-    ref = oracle.gemm(fmt, X, W, N)
-    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, axw, K))
-    refr = oracle.gemm(fmt, X, W, N, R=R)
-    tolerance.check(host(Yr), refr, tolerance.gemm_bound(refr, axw, K))
-    refh = oracle.gemm(fmt, X, W, N, head_D=D)
-    tolerance.check(host(Yh), refh, tolerance.gemm_bound(refh, axw.reshape(M, H, D).transpose(1, 0, 2), K))
+    tolerance.check_ref(host(Y), oracle.gemm(fmt, X, W, N), what="standard")
+    tolerance.check_ref(host(Yr), oracle.gemm(fmt, X, W, N, R=R), what="residual")
+    tolerance.check_ref(host(Yh), oracle.gemm(fmt, X, W, N, head_D=D), what="direct-head")
 
 
 def test_router_kernels_by_name(bridge, oracle):
@@ -164,8 +160,7 @@ def test_router_kernels_by_name(bridge, oracle):
                 assert np.array_equal(host(Y).view(np.uint16), host(Yf).view(np.uint16)), name
         if fmt == 3:
             Wh = host(W)
-            ref = oracle.gemm(3, X, Wh, N)
-            tolerance.check(host(Yf), ref, tolerance.gemm_bound(ref, absxw(oracle, 3, X, Wh, K, N), K))
+            tolerance.check_ref(host(Yf), oracle.gemm(3, X, Wh, N), what="ternary by name")
     W = dev(synth.random_blocks(0, N, K, 99))
     Y = empty16(M, N)
     with pytest.raises(RuntimeError, match="status code -3"):
@@ -210,6 +205,33 @@ def test_host_range_into_protected_page_returns_minus_5(bridge):
         buf.close()
 
 
+def test_chained_host_buffer_dispatches_without_synchronize(bridge, oracle):
+    """Host (pageable) buffers chained Y1 -> X2 with no synchronize between
+    the two dispatches: the second must read the first's result, as the
+    reference's in-order queue on zero-copy buffers gives it; also a host
+    residual R that is the first dispatch's output."""
+    M, K, N = 64, 256, 256
+    X = synth.activations(M, K, 301)
+    W1 = synth.quantized_weights(0, N, K, 302)
+    W2 = synth.quantized_weights(0, N, N, 303)
+    Y1 = np.full((M, N), 3.0, np.float16)
+    Y2 = np.zeros((M, N), np.float16)
+    Y3 = np.zeros((M, N), np.float16)
+    lib = bridge._lib
+    assert lib.m4_bridge_dispatch_gemm(X.ctypes.data, X.nbytes, W1.ctypes.data, W1.nbytes, Y1.ctypes.data,
+                                       Y1.nbytes, 0, M, K, N) == 0
+    assert lib.m4_bridge_dispatch_gemm(Y1.ctypes.data, Y1.nbytes, W2.ctypes.data, W2.nbytes, Y2.ctypes.data,
+                                       Y2.nbytes, 0, M, N, N) == 0
+    assert lib.m4_bridge_dispatch_gemm_residual(X.ctypes.data, X.nbytes, W1.ctypes.data, W1.nbytes,
+                                                Y1.ctypes.data, Y1.nbytes, Y3.ctypes.data, Y3.nbytes, 0, M, K,
+                                                N) == 0
+    bridge.synchronize()
+    ref1 = oracle.gemm(0, X, W1, N)
+    assert maxdiff(Y1, ref1) <= TOL
+    assert maxdiff(Y2, oracle.gemm(0, Y1, W2, N)) <= TOL
+    assert maxdiff(Y3, oracle.gemm(0, X, W1, N, R=Y1)) <= TOL
+
+
 def test_in_flight_buffers_retained_until_synchronize(bridge):
     """tests/redteam_bridge.py:486-528: the bridge holds the tensors of issued
     work until synchronize(), so dropping the caller's references is safe."""
@@ -246,8 +268,7 @@ def test_under_filled_grid_shapes(bridge, oracle, fmt, M, K, N):
     bridge.synchronize()
     rows = np.unique(np.r_[0, 1, 63, 64, 127, np.arange(0, M, 37), M - 1])
     Xs = np.ascontiguousarray(X[rows])
-    ref = oracle.gemm(fmt, Xs, W, N)
-    tolerance.check(host(Y)[rows], ref, tolerance.gemm_bound(ref, absxw(oracle, fmt, Xs, W, K, N), K))
+    tolerance.check_ref(host(Y)[rows], oracle.gemm(fmt, Xs, W, N), what=f"fmt {fmt} {M}x{K}x{N}")
     Y2 = empty16(M, N)
     bridge.dispatch_router_gemm(dev(X), dev(W), Y2, fmt, M, K, N)
     bridge.synchronize()
@@ -298,13 +319,9 @@ def test_gemm_q8_0_and_prism(bridge, oracle, fmt, M, K, N):
     with pytest.raises(RuntimeError):
         bridge.dispatch_gemm(dev(X), dev(W), empty16(M, N), fmt, M, K, N)
     bridge.synchronize()
-    axw = absxw(oracle, fmt, X, W, K, N)
-    ref = oracle.gemm(fmt, X, W, N)
-    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, axw, K))
-    refr = oracle.gemm(fmt, X, W, N, R=R)
-    tolerance.check(host(Yr), refr, tolerance.gemm_bound(refr, axw, K))
-    refh = oracle.gemm(fmt, X, W, N, head_D=D)
-    tolerance.check(host(Yh), refh, tolerance.gemm_bound(refh, axw.reshape(M, H, D).transpose(1, 0, 2), K))
+    tolerance.check_ref(host(Y), oracle.gemm(fmt, X, W, N), what="standard")
+    tolerance.check_ref(host(Yr), oracle.gemm(fmt, X, W, N, R=R), what="residual")
+    tolerance.check_ref(host(Yh), oracle.gemm(fmt, X, W, N, head_D=D), what="direct-head")
 
 
 # --------------------------------------------------------------------------
@@ -321,8 +338,7 @@ def test_gemm_tier1_shapes(bridge, oracle, fmt, M):
     Y = empty16(M, N)
     bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
     bridge.synchronize()
-    ref = oracle.gemm(fmt, X, W, N)
-    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, fmt, X, W, K, N), K))
+    tolerance.check_ref(host(Y), oracle.gemm(fmt, X, W, N), what=f"tier-1 fmt {fmt} M={M}")
 
 
 @pytest.mark.parametrize("fmt", [0, 1, 2, 3])
@@ -395,8 +411,7 @@ def test_gemv_and_misaligned_pointers(bridge, oracle):
     assert lib.m4_bridge_dispatch_gemv(xb.data_ptr() + 1, K * 2, wb.data_ptr(), W.size, yb.data_ptr(), N * 2, 2,
                                        K, N) == -2
     bridge.synchronize()
-    ref = oracle.gemm(2, x, W, N)[0]
-    tolerance.check(host(y), ref, tolerance.gemm_bound(ref, absxw(oracle, 2, x, W, K, N)[0], K))
+    tolerance.check_ref(host(y), oracle.gemm(2, x, W, N)[0], what="gemv")
     np.testing.assert_array_equal(host(yb)[1:], host(y))
 
 
@@ -404,7 +419,7 @@ def test_gemv_and_misaligned_pointers(bridge, oracle):
 def test_direct_head_and_residual(bridge, oracle, fmt):
     M, K, H, D = 129, 512, 4, 64
     N = H * D
-    X = synth.activations(M, K, 21)
+    X = synth.activations(M, K, 21, std=0.35)  # test_tier1_feature_coverage.mm:151-223 inputs
     W = synth.random_blocks(fmt, N, K, 22)
     Yh = empty16(H, M, D)
     bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
@@ -412,12 +427,8 @@ def test_direct_head_and_residual(bridge, oracle, fmt):
     Yr = empty16(M, N)
     bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
     bridge.synchronize()
-    axw = absxw(oracle, fmt, X, W, K, N)
-    ref = oracle.gemm(fmt, X, W, N)
-    refh = oracle.gemm(fmt, X, W, N, head_D=D)
-    tolerance.check(host(Yh), refh, tolerance.gemm_bound(ref, axw, K).reshape(M, H, D).transpose(1, 0, 2))
-    refr = oracle.gemm(fmt, X, W, N, R=R)
-    tolerance.check(host(Yr), refr, tolerance.gemm_bound(refr, axw, K))
+    tolerance.check_ref(host(Yh), oracle.gemm(fmt, X, W, N, head_D=D), what="direct-head")
+    tolerance.check_ref(host(Yr), oracle.gemm(fmt, X, W, N, R=R), what="residual")
 
 
 # --------------------------------------------------------------------------
@@ -439,7 +450,15 @@ def test_swiglu(bridge, oracle, fmt, M):
     Wgd, Wud = oracle.dequantize_f64(fmt, Wg, K, N), oracle.dequantize_f64(fmt, Wu, K, N)
     g, u = Xd @ Wgd.T, Xd @ Wud.T
     bound = tolerance.swiglu_bound(ref, g, u, np.abs(Xd) @ np.abs(Wgd).T, np.abs(Xd) @ np.abs(Wud).T, K)
-    tolerance.check(host(out), ref, bound)
+    if fmt == 2:
+        # Random Q4_K codes reach |w| ~ 2: the fp16 rounding of the weights
+        # alone (the bit-exact operands) moves silu(g) u by more than 1/128 at
+        # some |out| < 8 (a CPU model with exact fp16-weight products shows
+        # 0.018).  The reference checks SwiGLU only on Q4_0, at 0.05
+        # (brick3_swiglu_bench.mm:419), so this case keeps the error bound.
+        tolerance.check(host(out), ref, bound)
+    else:
+        tolerance.check_ref(host(out), ref, big_bound=bound, what=f"swiglu fmt {fmt}")
 
 
 @pytest.mark.parametrize("fmt", [0, 1, 2, 3])
@@ -623,8 +642,7 @@ def test_gguf_q4_k_tensor_feeds_the_projection(bridge, oracle):
     Y = empty16(M, N)
     bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
     bridge.synchronize()
-    ref = oracle.gemm(2, X, W, N)
-    tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, 2, X, W, K, N), K))
+    tolerance.check_ref(host(Y), oracle.gemm(2, X, W, N), what="gguf q4_k")
 
 
 # --------------------------------------------------------------------------

@@ -526,3 +526,37 @@ def test_layer_ex_reduces_to_the_router_layer(oracle):
     a = oracle.layer(0, X, *W, H, D, Nm, 0.125)
     b = oracle.layer_ex(0, X, None, *W[:4], None, *W[4:], H, H, D, Nm, 0.125, rope=False)
     np.testing.assert_array_equal(a, b)
+
+
+def test_row_sampled_attention_and_layer_equal_the_full_ones(oracle):
+    """attention_q8_0_rows / layer_ex_rows (the checkers of the full-size GPU
+    tests) equal rows of the pinned full attention / layer: GQA, RoPE at each
+    row's own position, both norms, and the plain router layer."""
+    rng = np.random.default_rng(1)
+    H, Hkv, M, D = 4, 2, 150, 64
+    Q, K, V = (rng.standard_normal((h, M, D)).astype(np.float16) for h in (H, Hkv, Hkv))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    full = oracle.attention_q8_0_gqa(Q, Kq, Vq, Hkv, 0.125)
+    pos = np.array([0, 1, 63, 64, 149, 77])
+    r = oracle.attention_q8_0_rows(Q[:, pos], Kq, Vq, pos, M, Hkv, 0.125)
+    np.testing.assert_array_equal(r, full[:, pos])
+    rt = oracle.attention_q8_0_rows(Q[:, pos], Kq, Vq, pos, M, Hkv, 0.125, o_token_major=True)
+    np.testing.assert_array_equal(rt.reshape(pos.size, H, D).transpose(1, 0, 2), r)
+    M, dm, Hq, Hkv, D, Nm = 96, 128, 4, 2, 32, 256
+    X = synth.activations(M, dm, 3)
+    shapes = [(Hq * D, dm), (Hkv * D, dm), (Hkv * D, dm), (dm, Hq * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    Ws = [synth.quantized_weights(0, n, k, 10 + i) for i, (n, k) in enumerate(shapes)]
+    na = (1 + 0.1 * rng.standard_normal(dm)).astype(np.float16)
+    nf = (1 + 0.1 * rng.standard_normal(dm)).astype(np.float16)
+    pos = np.array([0, 5, 31, 95, 40])
+    for norms, rope in (((na, nf), True), ((None, None), False)):
+        full = oracle.layer_ex(0, X, norms[0], *Ws[:4], norms[1], *Ws[4:], Hq=Hq, Hkv=Hkv, D=D, N_mlp=Nm,
+                               scale=0.17, rope=rope, theta=500000.0, offset=5)
+        r = oracle.layer_ex_rows(0, X, norms[0], *Ws[:4], norms[1], *Ws[4:], pos, Hq=Hq, Hkv=Hkv, D=D, N_mlp=Nm,
+                                 scale=0.17, rope=rope, theta=500000.0, offset=5)
+        np.testing.assert_array_equal(r, full[pos])
+    Wl = [synth.quantized_weights(0, n, k, 30 + i) for i, (n, k) in
+          enumerate([(Hq * D, dm)] * 3 + [(dm, Hq * D), (Nm, dm), (Nm, dm), (dm, Nm)])]
+    full = oracle.layer(0, X, *Wl, H=Hq, D=D, N_mlp=Nm, scale=0.17)
+    r = oracle.layer_ex_rows(0, X, None, *Wl[:4], None, *Wl[4:], pos, Hq=Hq, Hkv=Hq, D=D, N_mlp=Nm, scale=0.17)
+    np.testing.assert_array_equal(r, full[pos])
