@@ -269,13 +269,10 @@ int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, 
     return 0;
 }
 
-// Split-K workspace shared by the small-M and tiled kernels (launches are
-// ordered on the bridge stream): grow-only; counters are zeroed once at
-// allocation and every launch leaves them zeroed.
+// Split-K workspace (fp32 partials) shared by the small-M and tiled kernels;
+// launches are ordered on the bridge stream, grow-only.
 float* g_sk_ws = nullptr;
 size_t g_sk_ws_floats = 0;
-uint32_t* g_sk_cnt = nullptr;
-size_t g_sk_cnt_n = 0;
 
 // Makes `buf` hold at least `need` bytes.  Growing allocates a new buffer and
 // retires the old one (kept until shutdown: a graph captured before may
@@ -307,27 +304,21 @@ hipError_t grow(void** buf, size_t* bytes, size_t need, bool zero, const char* w
     return hipSuccess;
 }
 
-hipError_t ensure_skinny_ws(size_t floats, size_t groups) {
-    size_t wb = g_sk_ws_floats * sizeof(float), cb = g_sk_cnt_n * sizeof(uint32_t);
+hipError_t ensure_splitk_ws(size_t floats) {
+    size_t wb = g_sk_ws_floats * sizeof(float);
     void* w = g_sk_ws;
-    void* c = g_sk_cnt;
     hipError_t e = grow(&w, &wb, floats * sizeof(float), false, "split-K workspace");
-    if (e == hipSuccess) e = grow(&c, &cb, groups * sizeof(uint32_t), true, "split-K counters");
     g_sk_ws = static_cast<float*>(w);
     g_sk_ws_floats = wb / sizeof(float);
-    g_sk_cnt = static_cast<uint32_t*>(c);
-    g_sk_cnt_n = cb / sizeof(uint32_t);
     return e;
 }
 
 int launch(const qr::GemmParams& p0) {
     qr::GemmParams p = p0;
     if (qr::skinny_supported(p)) {
-        uint32_t ks = 0, groups = 0;
-        size_t floats = qr::skinny_workspace_floats(p.M, p.N, p.K, &ks, &groups);
-        hipError_t e = ensure_skinny_ws(floats ? floats : 1, groups);
-        if (e != hipSuccess) return staging_failed();
-        e = qr::launch_gemm_skinny(p, g_sk_ws, g_sk_cnt, g_stream);
+        const size_t floats = qr::skinny_workspace_floats(p.M, p.N, p.K);
+        if (ensure_splitk_ws(floats ? floats : 1) != hipSuccess) return staging_failed();
+        hipError_t e = qr::launch_gemm_skinny(p, g_sk_ws, g_stream);
         if (e != hipSuccess) {
             set_error("launch_gemm_skinny", e);
             return -6;
@@ -336,12 +327,8 @@ int launch(const qr::GemmParams& p0) {
     }
     p.ksplit = qr::gemm_pick_ksplit(p);
     if (p.ksplit > 1) {
-        uint32_t tiles = 0;
-        size_t floats = qr::gemm_workspace_floats(p, p.ksplit, &tiles);
-        hipError_t e = ensure_skinny_ws(floats, tiles);
-        if (e != hipSuccess) return staging_failed();
+        if (ensure_splitk_ws(qr::gemm_workspace_floats(p, p.ksplit)) != hipSuccess) return staging_failed();
         p.ws = g_sk_ws;
-        p.counters = g_sk_cnt;
     }
     hipError_t e = qr::launch_gemm(p, g_stream);
     if (e != hipSuccess) {
@@ -744,7 +731,7 @@ double m4_bridge_get_uma_footprint_mb(void) {
         fclose(f);
     }
     double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
-    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 + g_sk_cnt_n * 4 +
+    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 +
                               g_retired_bytes) /
                          (1024.0 * 1024.0);
 }
@@ -765,13 +752,11 @@ void m4_bridge_shutdown(void) {
     g_attn_ws = nullptr;
     g_attn_ws_bytes = 0;
     if (g_sk_ws) (void)hipFree(g_sk_ws);
-    if (g_sk_cnt) (void)hipFree(g_sk_cnt);
     for (void* r : g_retired) (void)hipFree(r);
     g_retired.clear();
     g_retired_bytes = 0;
     g_sk_ws = nullptr;
-    g_sk_cnt = nullptr;
-    g_sk_ws_floats = g_sk_cnt_n = 0;
+    g_sk_ws_floats = 0;
     if (g_own_stream) (void)hipStreamDestroy(g_own_stream);
     g_own_stream = nullptr;
     g_stream = nullptr;

@@ -7,10 +7,11 @@
 // 442-581) with its entry points (:588-927), and the fused dual-projection
 // SwiGLU swiglu_mma_dual_simd (brick3_swiglu_kernels.metal:428-698).
 //
-// One workgroup = NW wave64s and one BM x BN output tile (BM = 32 TM rows,
-// BN = NW x 32 TN columns).  The waves split the tile along N only, so every
-// weight column belongs to exactly one wave and is decoded exactly once per
-// workgroup:
+// One workgroup = NW wave64s and one BM x BN output tile, the waves arranged
+// as WR row groups x NW / WR column groups of 32 TM x 32 TN wave tiles.  With
+// WR = 1 every weight column belongs to exactly one wave and is decoded
+// exactly once per workgroup; WR = 2 decodes each column in two waves (one
+// per row group) for twice the waves per SIMD at the same tile:
 //  * K advances 64 per step = two 32-element quant groups per column.  For
 //    v_mfma_f32_32x32x16_f16 lane l supplies column l % 32 and the 8 k values
 //    8 (l / 32) .. +7 of each 16-wide slice; here the K order inside a step is
@@ -35,9 +36,9 @@
 //  * Epilogue: fp32 accumulators (+ fp16 residual, + SwiGLU for the dual
 //    variant) rounded once to fp16, staged through LDS for 16-byte stores,
 //    written [M, N] or head-major [H, M, D] (quant_router_kernels.metal:570-574).
-//    K split across workgroups: partials go to a workspace with agent-scope
-//    stores; the last workgroup of the tile (agent-scope counter) sums them in
-//    split order -- deterministic, one launch.
+//    K split across workgroups: each split writes fp32 partials to a
+//    workspace and a second, elementwise kernel sums them in split order and
+//    runs the same epilogue -- deterministic, ordered by the kernel boundary.
 #include "qr_decode.h"
 #include "qr_gemm_shapes.h"
 
@@ -56,12 +57,17 @@ namespace rb {
 constexpr int kBK = 64;
 constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
 
-template <int TM, int TN, int NW, bool DUAL>
+// NW waves as WR row groups x NW / WR column groups; a wave's tile is
+// 32 TM rows x 32 TN columns.
+template <int TM, int TN, int NW, int WR, bool DUAL>
 struct Cfg {
+    static_assert(NW % WR == 0, "whole column groups");
     static constexpr int NT = 64 * NW;
-    static constexpr int BM = 32 * TM;
+    static constexpr int WC = NW / WR;            // column groups
+    static constexpr int WM = 32 * TM;            // rows per wave
+    static constexpr int BM = WR * WM;
     static constexpr int WN = 32 * TN;            // columns per wave
-    static constexpr int BN = NW * WN;
+    static constexpr int BN = WC * WN;
     static constexpr int NCB = DUAL ? 2 * TN : TN;  // 32-column B tiles per wave (gate, then up)
     static constexpr int XCH = BM * kBK / 8;      // 16-byte X chunks per step
     static constexpr int XPT = (XCH + NT - 1) / NT;
@@ -95,10 +101,10 @@ __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt
 // set and batched partial loads need registers); the SwiGLU instance without
 // it is sized for QR_RB_DUAL_OCC workgroups per CU, so one workgroup's
 // prologue and epilogue overlap another's main loop.
-template <int F, int TM, int TN, int NW, bool DUAL, int P, bool SPLIT>
+template <int F, int TM, int TN, int NW, int WR, bool DUAL, int P, bool SPLIT>
 __global__ void __launch_bounds__(64 * NW, ((DUAL && !SPLIT) ? QR_RB_DUAL_OCC : 1))
 gemm_rb_kernel(GemmParams p) {
-    using C = rb::Cfg<TM, TN, NW, DUAL>;
+    using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
     using Dec = Decoder<F>;
     constexpr int NT = C::NT;
     constexpr int NCB = C::NCB;
@@ -109,6 +115,7 @@ gemm_rb_kernel(GemmParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int wrow = wave / C::WC, wcolg = wave % C::WC;  // this wave's row group and column group
     const int h = lane >> 5;     // quant group of the step this lane owns
     const int c32 = lane & 31;
 
@@ -147,7 +154,7 @@ gemm_rb_kernel(GemmParams p) {
     auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
 
     // local column of B tile jb for this lane
-    auto bcol = [&](int jb) { return wave * C::WN + (jb % TN) * 32 + c32; };
+    auto bcol = [&](int jb) { return wcolg * C::WN + (jb % TN) * 32 + c32; };
 
     // Pipelines (U = 6 steps unrolled, so every ring index below is static):
     //  X:  raw 16-byte chunks fetched 4 steps ahead into XP = 2 register slots,
@@ -212,7 +219,7 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < NCB; j++) acc[i][j] = f16v_t{};
 
-    const int arow = c32;
+    const int arow = wrow * C::WM + c32;
     const int akof = 32 * h;
     auto read_a = [&](int stage, int kk, h8_t out[TM]) {
         const _Float16* As = lds + stage * C::LDS_STAGE;
@@ -308,95 +315,30 @@ gemm_rb_kernel(GemmParams p) {
     for (int j = 0; j < U; j++)
         if (s0 + j < nsteps) step_body(s0 + j, j);
 
-    // ---- split-K: publish partials, the last workgroup of the tile sums ----
-    // Workspace slot of (split z, tile): ACC / 2 float pairs per thread, pair q
-    // of thread t at q * NT + t (coalesced across lanes).  Partials cross XCDs,
-    // whose L2s are not coherent with each other: they are written and read
-    // with 64-bit agent-scope atomics, published by a release / acquire pair
-    // around the tile counter; the reads are issued in batches of up to 32 so
-    // their latencies overlap.
+    // ---- split-K: this split's fp32 partial sums go to the workspace, laid
+    // out [split][plane][M][N] (plane 1: the SwiGLU up projection); the
+    // reduction kernel launched after this one (splitk_reduce_kernel) sums
+    // the splits in split order and runs the epilogue.  The kernel boundary
+    // orders the partials before their reads: no cross-workgroup
+    // synchronization inside the kernel.  Lanes 0..31 of a row store 128
+    // consecutive bytes. ----
     if (SPLIT && ksplit > 1) {
-        constexpr int NP = C::ACC / 2;                 // float pairs per thread
-        constexpr int BATCH = NP < 32 ? NP : 32;       // pairs in flight per batch
-        static_assert(NP % BATCH == 0 && BATCH % 8 == 0, "whole 32x32 tiles per batch");
-        const uint32_t T = nt_m * nt_n;
-        const uint32_t tile = tmi * nt_n + tni;
-        // tile row of accumulator element r of tile i (the pair r, r + 1 covers it and the next row)
-        auto pair_row = [&](int i, int r) { return 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
-        auto pair_ptr = [&](uint32_t z) {
-            return reinterpret_cast<uint64_t*>(p.ws) + ((size_t)z * T + tile) * (NP * NT) + tid;
-        };
-        {
-            uint64_t* dst = pair_ptr(kz);
-            int q = 0;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < NCB; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r += 2, q++) {
-                        const uint64_t v = (uint64_t)f32_bits(acc[i][j][r]) | ((uint64_t)f32_bits(acc[i][j][r + 1]) << 32);
-                        if (pair_row(i, r) < mrows)  // rows past M are never written out
-                            __hip_atomic_store(dst + q * NT, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-        }
-        // Publication: every thread's partial stores are released at agent
-        // scope before the workgroup barrier; thread 0's counter increment is
-        // an agent-scope acq_rel RMW, so the last arriver's acquire fence
-        // below makes every split's partials visible to all its threads.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        __shared__ uint32_t s_last;
-        if (tid == 0) {
-            const uint32_t prev =
-                __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = (prev == ksplit - 1) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // sum all splits in split order (deterministic); this workgroup's own
-        // split comes from its registers, the others from the workspace
-        f16v_t tot[TM][NCB];
+        const size_t plane = (size_t)M * N;
+        float* base = p.ws + (size_t)kz * plane * (DUAL ? 2 : 1);
+        const int r0 = m0 + wrow * C::WM, c0 = n0 + wcolg * C::WN;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < NCB; j++) tot[i][j] = f16v_t{};
-        for (uint32_t z = 0; z < ksplit; z++) {
-            if (z == kz) {
+            for (int jb = 0; jb < NCB; jb++) {
+                const int n = c0 + (jb % TN) * 32 + c32;
+                float* pl = base + (DUAL && jb >= TN ? plane : 0);
 #pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < NCB; j++) tot[i][j] += acc[i][j];
-                continue;
-            }
-            const uint64_t* src = pair_ptr(z);
-#pragma unroll
-            for (int q0 = 0; q0 < NP; q0 += BATCH) {
-                uint64_t t[BATCH];
-#pragma unroll
-                for (int q = 0; q < BATCH; q++) {
-                    const int qq = q0 + q;
-                    t[q] = pair_row((qq / 8) / NCB, 2 * (qq % 8)) < mrows
-                               ? __hip_atomic_load(src + qq * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                               : 0ull;
-                }
-#pragma unroll
-                for (int q = 0; q < BATCH; q++) {
-                    const int qq = q0 + q;               // pair index: tile qq / 8, rows 2 (qq % 8)
-                    const int i = (qq / 8) / NCB, j = (qq / 8) % NCB, r = 2 * (qq % 8);
-                    tot[i][j][r] += bits_f32((uint32_t)t[q]);
-                    tot[i][j][r + 1] += bits_f32((uint32_t)(t[q] >> 32));
+                for (int r = 0; r < 16; r++) {
+                    const int m = r0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m < (int)M && n < (int)N) pl[(size_t)m * N + n] = acc[i][jb][r];
                 }
             }
-        }
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < NCB; j++) acc[i][j] = tot[i][j];
-        // every split has arrived: no other workgroup touches this counter
-        // until the next launch, which the stream orders after this one
-        if (tid == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
     }
 
     // ---- epilogue: accumulator element r of lane l is row 8 (r / 4) + 4 (l / 32)
@@ -412,7 +354,8 @@ gemm_rb_kernel(GemmParams p) {
         }
         return v;
     };
-    const int wcol0 = n0 + wave * C::WN;
+    const int wcol0 = n0 + wcolg * C::WN;
+    const int wrow0 = m0 + wrow * C::WM;
     const bool vec_io = ((reinterpret_cast<uintptr_t>(p.Y) | reinterpret_cast<uintptr_t>(p.R)) & 15u) == 0 &&
                         (N & 7u) == 0 && (p.head_D & 7u) == 0;
     if (vec_io) {
@@ -434,7 +377,7 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
             for (int c = lane; c < CHUNKS; c += 64) {
                 const int row = c / (WC / 8), c8 = c % (WC / 8);
-                const int m = m0 + i * 32 + row;
+                const int m = wrow0 + i * 32 + row;
                 const int n = wcol0 + c8 * 8;
                 if (m < (int)M && n < (int)N) {
                     const f4_t lo = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8);
@@ -476,7 +419,7 @@ gemm_rb_kernel(GemmParams p) {
             const int n = wcol0 + j * 32 + c32;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = wrow0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < (int)M && n < (int)N) {
                     float v = value(i, j, r);
                     if (p.R) v += (float)p.R[(size_t)m * N + n];
@@ -494,11 +437,11 @@ gemm_rb_kernel(GemmParams p) {
 }
 
 
-template <int F, int TM, int TN, int NW, bool DUAL>
+template <int F, int TM, int TN, int NW, int WR, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
-    using C = rb::Cfg<TM, TN, NW, DUAL>;
-    auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES, true>
-                             : gemm_rb_kernel<F, TM, TN, NW, DUAL, QR_RB_STAGES, false>;
+    using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
+    auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, QR_RB_STAGES, true>
+                             : gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, QR_RB_STAGES, false>;
     const size_t lds = C::LDS_BYTES;
     const uint32_t ntm = (p.M + C::BM - 1) / C::BM;
     uint32_t T = ntm * ((p.N + C::BN - 1) / C::BN);
@@ -512,6 +455,8 @@ template <int F, bool DUAL>
 static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
     if constexpr (DUAL) {
         return rb_launch_cfg<F, QR_RB_DUAL, true>(p, st);
+    } else if constexpr (F == QUANT_VAR_RATE_AFFINE || F == QUANT_EXL3) {
+        return rb_launch_cfg<F, QR_RB_MID, false>(p, st);  // rb_pick's only shape for these formats
     } else {
         switch (rb_pick(F, p.M, p.N, false)) {
             case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);

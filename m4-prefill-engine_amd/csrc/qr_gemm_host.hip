@@ -1,12 +1,67 @@
 // qr_gemm_host.hip -- host side of the tiled projection: format dispatch,
-// split-K choice and workspace sizing (kernels in qr_gemm.hip).
+// split-K choice and workspace sizing (kernels in qr_gemm.hip), and the
+// split-K reduction kernel shared with the small-M kernel.
+#include "qr_device.h"
 #include "qr_gemm_shapes.h"
 
 namespace qr {
 
-hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
-    GemmParams p = p0;
-    p.group_m = gemm_group_m(p);
+// Split-K reduction: out[m, n] = epilogue(sum over splits z = 0, 1, ... of
+// ws[z][plane][m][n]) with the tiled kernel's epilogue arithmetic (SwiGLU
+// silu(g) u in fp32 for DUAL, + fp16 residual, one rounding to fp16,
+// [M, N] or head-major [N / head_D, M, head_D]).  The splits are summed in
+// split order starting from 0, so the result does not depend on which
+// workgroup finished first.  Four consecutive elements per thread.
+template <bool DUAL>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ ws, uint32_t ks, uint32_t M,
+                                                            uint32_t N, const _Float16* __restrict__ R,
+                                                            _Float16* __restrict__ Y, uint32_t head_D) {
+    const size_t plane = (size_t)M * N;
+    const size_t e0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e0 >= plane) return;
+    const int cnt = plane - e0 < 4 ? (int)(plane - e0) : 4;
+    const bool vec = cnt == 4 && (N & 3u) == 0;  // four elements of one row, 16-byte aligned
+    float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t z = 0; z < ks; z++) {
+        const float* src = ws + (size_t)z * plane * (DUAL ? 2 : 1) + e0;
+        if (vec) {
+            const f4_t a = *reinterpret_cast<const f4_t*>(src);
+            g[0] += a.x; g[1] += a.y; g[2] += a.z; g[3] += a.w;
+            if constexpr (DUAL) {
+                const f4_t b = *reinterpret_cast<const f4_t*>(src + plane);
+                u[0] += b.x; u[1] += b.y; u[2] += b.z; u[3] += b.w;
+            }
+        } else {
+            for (int q = 0; q < cnt; q++) {
+                g[q] += src[q];
+                if constexpr (DUAL) u[q] += src[plane + q];
+            }
+        }
+    }
+    for (int q = 0; q < cnt; q++) {
+        const size_t e = e0 + q;
+        const uint32_t m = (uint32_t)(e / N), n = (uint32_t)(e % N);
+        float v = g[q];
+        if constexpr (DUAL) v = v / (1.0f + __expf(-v)) * u[q];
+        if (R) v += (float)R[e];
+        size_t o = e;
+        if (head_D) o = ((size_t)(n / head_D) * M + m) * head_D + n % head_D;
+        Y[o] = (_Float16)v;
+    }
+}
+
+hipError_t launch_splitk_reduce(const float* ws, uint32_t ks, uint32_t M, uint32_t N, bool dual, const _Float16* R,
+                                _Float16* Y, uint32_t head_D, hipStream_t st) {
+    const size_t plane = (size_t)M * N;
+    const unsigned blocks = (unsigned)((plane + 1023) / 1024);
+    if (dual)
+        hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(blocks), dim3(256), 0, st, ws, ks, M, N, R, Y, head_D);
+    else
+        hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(blocks), dim3(256), 0, st, ws, ks, M, N, R, Y, head_D);
+    return hipGetLastError();
+}
+
+static hipError_t launch_gemm_main(const GemmParams& p, hipStream_t st) {
     switch (p.format) {
         case QUANT_Q4_0: return launch_gemm_format<QUANT_Q4_0>(p, st);
         case QUANT_MLX_4BIT: return launch_gemm_format<QUANT_MLX_4BIT>(p, st);
@@ -18,6 +73,15 @@ hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
         case QUANT_PRISM_Q2_0: return launch_gemm_format<QUANT_PRISM_Q2_0>(p, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
+    GemmParams p = p0;
+    p.group_m = gemm_group_m(p);
+    hipError_t e = launch_gemm_main(p, st);
+    if (e == hipSuccess && p.ksplit > 1)
+        e = launch_splitk_reduce(p.ws, p.ksplit, p.M, p.N, p.W2 != nullptr, p.R, p.Y, p.head_D, st);
+    return e;
 }
 
 static uint32_t tiles_of(const GemmParams& p, const RbShape& d) {
@@ -47,12 +111,8 @@ uint32_t gemm_pick_ksplit(const GemmParams& p) {
     return ks;
 }
 
-size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks, uint32_t* tiles) {
-    const bool dual = p.W2 != nullptr;
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, dual));
-    const uint32_t T = ((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
-    if (tiles) *tiles = T;
-    return ks > 1 ? (size_t)ks * T * d.bm * d.bn * (dual ? 2 : 1) : 0;
+size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks) {
+    return ks > 1 ? (size_t)ks * p.M * p.N * (p.W2 != nullptr ? 2 : 1) : 0;
 }
 
 uint32_t gemm_group_m(const GemmParams& p) {

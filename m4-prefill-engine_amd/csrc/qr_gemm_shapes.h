@@ -6,7 +6,8 @@
 
 namespace qr {
 
-// Shapes {TM, TN, NW}: BM = 32 TM, BN = 32 TN NW.
+// Shapes {TM, TN, NW, WR}: NW waves in WR row groups; BM = 32 TM WR,
+// BN = 32 TN NW / WR.
 //   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K: QR_RB_BIG_K,
 //                  default 4, 1, 8 -> 128 x 256 with two waves per SIMD, whose
 //                  heavier decode then overlaps the other wave's MFMAs)
@@ -17,22 +18,22 @@ namespace qr {
 //                  computes 192 rows, not 256)
 //   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
 #ifndef QR_RB_BIG
-#define QR_RB_BIG 4, 2, 4
+#define QR_RB_BIG 4, 2, 4, 1
 #endif
 #ifndef QR_RB_BIG_K
-#define QR_RB_BIG_K 4, 1, 8
+#define QR_RB_BIG_K 4, 1, 8, 1
 #endif
 #ifndef QR_RB_MID
-#define QR_RB_MID 4, 1, 4
+#define QR_RB_MID 4, 1, 4, 1
 #endif
 #ifndef QR_RB_MID64
-#define QR_RB_MID64 2, 1, 4
+#define QR_RB_MID64 2, 1, 4, 1
 #endif
 #ifndef QR_RB_DUAL
-#define QR_RB_DUAL 4, 1, 4
+#define QR_RB_DUAL 4, 1, 4, 1
 #endif
-template <int TM, int TN, int NW> struct ShapeOf {
-    static constexpr uint32_t bm = 32 * TM, bn = 32 * TN * NW;
+template <int TM, int TN, int NW, int WR> struct ShapeOf {
+    static constexpr uint32_t bm = 32 * TM * WR, bn = 32 * TN * (NW / WR);
 };
 struct RbShape {
     uint32_t bm, bn;
@@ -46,6 +47,9 @@ struct RbShape {
 // extra split -- is halved or avoided.
 inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     if (dual) return 2;
+    // The 3/5-bit double-rounding formats (no BASELINE configuration) keep
+    // one tile shape: fewer instances of their heavy fp64 decode to compile.
+    if (format == QUANT_VAR_RATE_AFFINE || format == QUANT_EXL3) return 1;
     if (M >= 1024) {
         if (format == QUANT_Q4_K) return 3;
         const uint32_t big_tiles = ((M + 127) / 128) * ((N + 255) / 256);
@@ -58,6 +62,10 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     const bool cheap = format == QUANT_Q4_0 || format == QUANT_MLX_4BIT || format == QUANT_TERNARY_1_58 ||
                        format == QUANT_Q8_0 || format == QUANT_PRISM_Q2_0;
     const uint32_t tail = M % 128;
+#ifdef QR_RB_MID64_FILL
+    // 64-row tiles whenever 128-row tiles leave the CUs under-filled
+    if (cheap && ((M + 127) / 128) * ((N + 127) / 128) < 256) return 4;
+#endif
     return (cheap && tail != 0 && tail <= 64) ? 4 : 1;
 }
 inline RbShape rb_dims(int s) {

@@ -18,11 +18,10 @@
 //    from LDS and decodes them to binary16 in registers (bit-exact vs the CPU
 //    unpack); activations are the B operand, 16 rows per tile, reused across
 //    the wave's 4 column tiles;
-//  * partial sums: the 8 waves reduce through LDS in a fixed order; KSPLIT
-//    workgroups of one column group write fp32 partials to a workspace with
-//    agent-scope stores and the last to arrive (agent-scope counter) sums them
-//    in split order, rounds once to fp16 and resets the counter --
-//    deterministic, one launch, no L2 writeback/invalidate.
+//  * partial sums: the 8 waves reduce through LDS in a fixed order; with a K
+//    split, each workgroup writes its fp32 partials to a workspace and the
+//    split-K reduction kernel (qr_gemm_host.hip) sums the splits in split
+//    order and rounds once to fp16 -- deterministic.
 #include "qr_device.h"
 #include "qr_formats.h"
 #include "qr_kernels.h"
@@ -195,8 +194,7 @@ __host__ __device__ inline SkLayout sk_layout(uint32_t M, uint32_t gpw, uint32_t
 }
 
 template <int F, int MT, int GPW>  // MT: 16-row tiles of M; GPW: 32-groups per wave
-__global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* ws, uint32_t* counters,
-                                                          uint32_t ksplit) {
+__global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* ws, uint32_t ksplit) {
     using FR = Frag<F>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr uint32_t GB = GroupBytes<F>::v;
@@ -312,88 +310,36 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
     __syncthreads();
 
     const bool split = ksplit > 1;
-    __shared__ uint32_t s_last;
     constexpr int NEL = ROWS * kSkCols;
     constexpr int PER = (NEL + 511) / 512;  // outputs per thread; element idx -> (m = idx / 64, n = idx % 64)
-    float tot[PER];
+    // K split: this split's fp32 partials go to ws [split][M][N] and
+    // splitk_reduce_kernel (launched next) sums them in split order;
+    // otherwise the sum is the output.
+    float* part = split ? ws + (size_t)ks * M * N : nullptr;
 #pragma unroll
     for (int e = 0; e < PER; e++) {
         const int idx = tid + 512 * e;
-        const int off = (idx / kSkCols) * RS + idx % kSkCols;
-        float s = 0.0f;
-        if (idx < NEL) {
-#pragma unroll
-            for (int w = 0; w < kSkWaves; w++) s += red[w * ROWS * RS + off];
-        }
-        tot[e] = s;
-    }
-
-    auto emit = [&](int idx, float v) {
         const uint32_t m = idx / kSkCols, nl = idx % kSkCols;
+        if (idx >= NEL || m >= M || nl >= ncols) continue;
+        const int off = (idx / kSkCols) * RS + idx % kSkCols;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kSkWaves; w++) v += red[w * ROWS * RS + off];
         const uint32_t n = n0 + nl;
-        if (idx < NEL && m < M && nl < ncols) {
-            if (p.R) v += (float)p.R[(size_t)m * N + n];
-            size_t o;
-            if (p.head_D) {
-                const uint32_t h = n / p.head_D, dd = n % p.head_D;
-                o = ((size_t)h * M + m) * p.head_D + dd;
-            } else {
-                o = (size_t)m * N + n;
-            }
-            p.Y[o] = (_Float16)v;
+        if (split) {
+            part[(size_t)m * N + n] = v;
+            continue;
         }
-    };
-
-    if (!split) {
-#pragma unroll
-        for (int e = 0; e < PER; e++) emit(tid + 512 * e, tot[e]);
-        return;
-    }
-
-    // ---- cross-workgroup split-K: partial slot ks, last arriver sums ----
-    // Partials are written with agent-scope atomic stores (coherent across
-    // XCDs) and published by a release / acquire pair around the column
-    // group's counter.
-    float* slot = ws + ((size_t)ks * gridDim.x + cg) * NEL;
-#pragma unroll
-    for (int e = 0; e < PER; e++)
-        if (tid + 512 * e < NEL)
-            __hip_atomic_store(slot + tid + 512 * e, tot[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // release the partials (agent scope) before the barrier; the counter RMW
-    // is acq_rel and the last arriver acquires before reading the others'
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(counters + cg, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == ksplit - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // Sum the split partials in split order; four splits' loads are issued
-    // together (indices clamped, not branched) so their latencies overlap.
-    static_assert(NEL % 512 == 0, "whole rows of outputs per thread");
-    float sum[PER];
-#pragma unroll
-    for (int e = 0; e < PER; e++) sum[e] = 0.0f;
-    for (uint32_t k0 = 0; k0 < ksplit; k0 += 4) {
-        float v[4][PER];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t k2 = min(k0 + j, ksplit - 1);
-            const float* src = ws + ((size_t)k2 * gridDim.x + cg) * NEL + tid;
-#pragma unroll
-            for (int e = 0; e < PER; e++)
-                v[j][e] = __hip_atomic_load(src + 512 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (p.R) v += (float)p.R[(size_t)m * N + n];
+        size_t o;
+        if (p.head_D) {
+            const uint32_t h = n / p.head_D, dd = n % p.head_D;
+            o = ((size_t)h * M + m) * p.head_D + dd;
+        } else {
+            o = (size_t)m * N + n;
         }
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < PER; e++) sum[e] += (k0 + j < ksplit) ? v[j][e] : 0.0f;
+        p.Y[o] = (_Float16)v;
     }
-#pragma unroll
-    for (int e = 0; e < PER; e++) emit(tid + 512 * e, sum[e]);
-    if (tid == 0) __hip_atomic_store(counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 static uint32_t group_bytes_rt(int f) {
@@ -427,20 +373,17 @@ static bool sk_plan(int f, uint32_t M, uint32_t N, uint32_t K, uint32_t* ks_out,
     return false;
 }
 
-size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K, uint32_t* ksplit_out, uint32_t* groups_out) {
+size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K) {
     uint32_t ks_max = 1;
     for (int f = 0; f < 4; f++) {
         uint32_t ks = 1, gpw = 1;
         if (sk_plan(f, M, N, K, &ks, &gpw) && ks > ks_max) ks_max = ks;
     }
-    const uint32_t groups = (N + kSkCols - 1) / kSkCols;
-    if (ksplit_out) *ksplit_out = ks_max;
-    if (groups_out) *groups_out = groups;
-    return ks_max > 1 ? (size_t)ks_max * groups * ((M + 15) / 16) * 16 * kSkCols : 0;
+    return ks_max > 1 ? (size_t)ks_max * M * N : 0;
 }
 
 template <int F, int MT, int GPW>
-static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t* counters, uint32_t ks, hipStream_t st) {
+static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t ks, hipStream_t st) {
     auto kern = gemm_skinny_kernel<F, MT, GPW>;
     const uint32_t groups = (p.N + kSkCols - 1) / kSkCols;
     const size_t lds = sk_layout(p.M, GPW, GroupBytes<F>::v).lds;
@@ -450,30 +393,31 @@ static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t* counters, 
         if (e != hipSuccess) return e;
         attr = lds;
     }
-    hipLaunchKernelGGL(kern, dim3(groups, ks), dim3(512), lds, st, p, ws, counters, ks);
-    return hipGetLastError();
+    hipLaunchKernelGGL(kern, dim3(groups, ks), dim3(512), lds, st, p, ws, ks);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && ks > 1) e = launch_splitk_reduce(ws, ks, p.M, p.N, false, p.R, p.Y, p.head_D, st);
+    return e;
 }
 
 template <int F, int MT>
-static hipError_t launch_sk_g(const GemmParams& p, float* ws, uint32_t* counters, uint32_t ks, uint32_t gpw,
-                              hipStream_t st) {
+static hipError_t launch_sk_g(const GemmParams& p, float* ws, uint32_t ks, uint32_t gpw, hipStream_t st) {
     switch (gpw) {
-        case 1: return launch_sk<F, MT, 1>(p, ws, counters, ks, st);
-        case 2: return launch_sk<F, MT, 2>(p, ws, counters, ks, st);
-        case 4: return launch_sk<F, MT, 4>(p, ws, counters, ks, st);
+        case 1: return launch_sk<F, MT, 1>(p, ws, ks, st);
+        case 2: return launch_sk<F, MT, 2>(p, ws, ks, st);
+        case 4: return launch_sk<F, MT, 4>(p, ws, ks, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int F>
-static hipError_t launch_sk_m(const GemmParams& p, float* ws, uint32_t* counters, hipStream_t st) {
+static hipError_t launch_sk_m(const GemmParams& p, float* ws, hipStream_t st) {
     uint32_t ks = 0, gpw = 0;
     if (!sk_plan(F, p.M, p.N, p.K, &ks, &gpw)) return hipErrorInvalidValue;
     switch ((p.M + 15) / 16) {
-        case 1: return launch_sk_g<F, 1>(p, ws, counters, ks, gpw, st);
-        case 2: return launch_sk_g<F, 2>(p, ws, counters, ks, gpw, st);
-        case 3: return launch_sk_g<F, 3>(p, ws, counters, ks, gpw, st);
-        case 4: return launch_sk_g<F, 4>(p, ws, counters, ks, gpw, st);
+        case 1: return launch_sk_g<F, 1>(p, ws, ks, gpw, st);
+        case 2: return launch_sk_g<F, 2>(p, ws, ks, gpw, st);
+        case 3: return launch_sk_g<F, 3>(p, ws, ks, gpw, st);
+        case 4: return launch_sk_g<F, 4>(p, ws, ks, gpw, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -485,12 +429,12 @@ bool skinny_supported(const GemmParams& p) {
     return sk_plan(p.format, p.M, p.N, p.K, &ks, &gpw);
 }
 
-hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, uint32_t* counters, hipStream_t st) {
+hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, hipStream_t st) {
     switch (p.format) {
-        case QUANT_Q4_0: return launch_sk_m<QUANT_Q4_0>(p, ws, counters, st);
-        case QUANT_MLX_4BIT: return launch_sk_m<QUANT_MLX_4BIT>(p, ws, counters, st);
-        case QUANT_Q4_K: return launch_sk_m<QUANT_Q4_K>(p, ws, counters, st);
-        case QUANT_TERNARY_1_58: return launch_sk_m<QUANT_TERNARY_1_58>(p, ws, counters, st);
+        case QUANT_Q4_0: return launch_sk_m<QUANT_Q4_0>(p, ws, st);
+        case QUANT_MLX_4BIT: return launch_sk_m<QUANT_MLX_4BIT>(p, ws, st);
+        case QUANT_Q4_K: return launch_sk_m<QUANT_Q4_K>(p, ws, st);
+        case QUANT_TERNARY_1_58: return launch_sk_m<QUANT_TERNARY_1_58>(p, ws, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -17,11 +17,10 @@ struct GemmParams {
     uint32_t head_D;      // 0: Y is [M, N]; else direct-head [N / head_D, M, head_D]
     size_t col_bytes;     // bytes of one weight column
     // K split across workgroups (tiled kernel): 0/1 = none.  `ws` holds
-    // gemm_workspace_floats() floats, `counters` one zeroed uint32 per tile
-    // (left zeroed on return).
+    // gemm_workspace_floats() floats of fp32 partials [split][plane][M][N];
+    // launch_gemm follows the projection with the reduction kernel.
     uint32_t ksplit;
     float* ws;
-    uint32_t* counters;
     uint32_t group_m;     // row-tiles per XCD tile group (0: kernel default)
     // Grouped launch: up to two more projections of the same X (same K,
     // format, head_D; no residual, no SwiGLU, no K split) in the same grid,
@@ -37,15 +36,19 @@ uint32_t gemm_group_m(const GemmParams& p);
 uint32_t gemm_pick_ksplit(const GemmParams& p);
 // Whether launch_gemm can run p's groups (ngroups >= 2) as one grid.
 bool gemm_grouped_ok(const GemmParams& p);
-size_t gemm_workspace_floats(const GemmParams& p, uint32_t ksplit, uint32_t* tiles);
+size_t gemm_workspace_floats(const GemmParams& p, uint32_t ksplit);
+// Sums split-K partials ws [ks][dual ? 2 : 1][M][N] in split order and writes
+// the projection epilogue (SwiGLU when dual, + R, fp16, head-major when
+// head_D) -- the second kernel of every split-K projection.
+hipError_t launch_splitk_reduce(const float* ws, uint32_t ks, uint32_t M, uint32_t N, bool dual, const _Float16* R,
+                                _Float16* Y, uint32_t head_D, hipStream_t st);
 
 // Small-M weight-streaming projection (M <= 64, no SwiGLU).  `ws` holds
-// skinny_workspace_floats() floats of split-K partials; `counters` one zeroed
-// uint32 per 64-column group (left zeroed on return).  Calls that share ws /
-// counters must be ordered on one stream.
+// skinny_workspace_floats() floats of split-K partials [split][M][N], summed
+// by launch_splitk_reduce.  Calls that share ws must be ordered on one stream.
 bool skinny_supported(const GemmParams& p);
-size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K, uint32_t* ksplit, uint32_t* groups);
-hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, uint32_t* counters, hipStream_t st);
+size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K);
+hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, hipStream_t st);
 hipError_t launch_dequant(int format, const uint8_t* W, _Float16* out, uint32_t K, uint32_t N, size_t col_bytes,
                           hipStream_t st);
 

@@ -27,7 +27,9 @@ def oracle():
 
 @pytest.fixture(scope="session")
 def libpath():
-    p = PKG / "libm4_bridge.so"
+    import os
+
+    p = Path(os.environ.get("M4_BRIDGE_LIB_PATH") or PKG / "libm4_bridge.so")
     if not p.exists():
         pytest.fail("libm4_bridge.so is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
     return p

@@ -632,13 +632,14 @@ def test_gguf_q4_k_tensor_feeds_the_projection(bridge, oracle):
     rng = np.random.default_rng(31)
     M, K, N = 129, 1024, 192
     nb = N * K // 256
-    q4k = ggml_pack_q4_k((rng.random(nb) * 0.004 + 1e-4).astype(np.float16), (rng.random(nb) * 0.004).astype(np.float16),
+    # super-block scales of real Q4_K checkpoints' magnitude (|w| <~ 1)
+    q4k = ggml_pack_q4_k((rng.random(nb) * 0.0004 + 1e-5).astype(np.float16), (rng.random(nb) * 0.0004).astype(np.float16),
                          rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8)), rng.integers(0, 16, (nb, 256)))
     ld = gguf.GGUFLoader()
     assert ld.parse_from_buffer(make_gguf([], [("blk.0.ffn_up.weight", [K, N], gguf.GGML_Q4_K, q4k.tobytes())]))
     W, fmt, k, n = ld.load_router_weights("blk.0.ffn_up.weight")
     assert (fmt, k, n) == (2, K, N)
-    X = synth.activations(M, K, 32)
+    X = synth.activations(M, K, 32, std=0.35)
     Y = empty16(M, N)
     bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
     bridge.synchronize()
