@@ -194,6 +194,21 @@ M4_API int m4_bridge_prefill_layer_ex(void* X_ptr, void* w_attn, void* Wq, void*
 M4_API int m4_bridge_dequantize(void* W_ptr, size_t W_bytes, void* out_ptr, size_t out_bytes, int format,
                          uint32_t K, uint32_t N);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): m4_bridge_dispatch_gemm's projection with the same
+ * arguments, validation and results, but its split-K partials live in a
+ * fixed 32 MiB device scratch array of the library (one per GPU, held until
+ * the process ends) and no device memory is allocated or freed.  X, W and Y
+ * must be device memory (X and W 16-byte aligned): -2 otherwise, since host
+ * or misaligned buffers would need staging copies.  -4 when the shape needs
+ * more split-K partials than the scratch holds (ksplit * M * N <= 8 Mi
+ * floats: every tiled launch fits; small-M launches with long K and wide N,
+ * e.g. M = 48, K = 16384, N = 12288, do not).  Calls on one GPU share the scratch: calls
+ * that overlap in time (other streams, other threads' streams) race. */
+M4_API int m4_bridge_dispatch_gemm_noalloc(void* X_ptr, size_t X_bytes, void* W_ptr, size_t W_bytes, void* Y_ptr,
+                                           size_t Y_bytes, int format, uint32_t M, uint32_t K, uint32_t N);
+
 /* Run subsequent work on `stream` (a hipStream_t, e.g. torch's current
  * stream); NULL restores the bridge's own stream.  Returns 0 or -1. */
 M4_API int m4_bridge_set_stream(void* stream);

@@ -313,12 +313,33 @@ hipError_t ensure_splitk_ws(size_t floats) {
     return e;
 }
 
-int launch(const qr::GemmParams& p0) {
+// Launches projection p.  Split-K partials go to `fixed_ws` (capacity
+// `fixed_floats`) when given -- the no-allocation entry point's scratch --
+// else to the bridge's grow-only workspace.  -4 when p needs more than the
+// fixed capacity.
+int launch_ws(const qr::GemmParams& p0, float* fixed_ws, size_t fixed_floats) {
     qr::GemmParams p = p0;
+    auto workspace = [&](size_t floats, float** ws) -> int {
+        if (fixed_ws) {
+            if (floats > fixed_floats) {
+                char buf[160];
+                snprintf(buf, sizeof(buf), "split-K partials need %zu floats, the fixed scratch holds %zu", floats,
+                         fixed_floats);
+                g_last_error = buf;
+                return -4;
+            }
+            *ws = fixed_ws;
+            return 0;
+        }
+        if (ensure_splitk_ws(floats) != hipSuccess) return staging_failed();
+        *ws = g_sk_ws;
+        return 0;
+    };
     if (qr::skinny_supported(p)) {
         const size_t floats = qr::skinny_workspace_floats(p.M, p.N, p.K);
-        if (ensure_splitk_ws(floats ? floats : 1) != hipSuccess) return staging_failed();
-        hipError_t e = qr::launch_gemm_skinny(p, g_sk_ws, g_stream);
+        float* ws = nullptr;
+        if (int rc = workspace(floats ? floats : 1, &ws)) return rc;
+        hipError_t e = qr::launch_gemm_skinny(p, ws, g_stream);
         if (e != hipSuccess) {
             set_error("launch_gemm_skinny", e);
             return -6;
@@ -327,8 +348,7 @@ int launch(const qr::GemmParams& p0) {
     }
     p.ksplit = qr::gemm_pick_ksplit(p);
     if (p.ksplit > 1) {
-        if (ensure_splitk_ws(qr::gemm_workspace_floats(p, p.ksplit)) != hipSuccess) return staging_failed();
-        p.ws = g_sk_ws;
+        if (int rc = workspace(qr::gemm_workspace_floats(p, p.ksplit), &p.ws)) return rc;
     }
     hipError_t e = qr::launch_gemm(p, g_stream);
     if (e != hipSuccess) {
@@ -337,6 +357,8 @@ int launch(const qr::GemmParams& p0) {
     }
     return 0;
 }
+
+int launch(const qr::GemmParams& p) { return launch_ws(p, nullptr, 0); }
 
 int gemm_common(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, void* R, int format, uint32_t M,
                 uint32_t K, uint32_t N, uint32_t head_D, bool ext) {
@@ -364,6 +386,20 @@ int gemm_common(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, void
     return finish(launch(p));
 }
 
+// ---- scratch of the no-allocation projection entry point ----
+// Split-K partials of m4_bridge_dispatch_gemm_noalloc live in this
+// file-scope device array (32 MiB, held on every GPU the library runs on
+// until the process ends): enough for every tiled launch (at most 256
+// workgroups of at most 128 x 256 outputs, so ksplit * M * N <= 8 Mi).  In host code `scratch` names a host-side stand-in
+// only: its device address, per device, comes from hipGetSymbolAddress at
+// init and is the only handle host code passes on.  Nothing in it has to
+// start at zero: every split writes all of its partials before the
+// reduction kernel reads them.
+constexpr size_t kScratchFloats = (size_t)8 << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
+constexpr int kMaxDevices = 64;
+float* g_scratch[kMaxDevices] = {};
+
 }  // namespace
 
 extern "C" {
@@ -385,6 +421,16 @@ bool m4_bridge_init(const char* /*metallib_path*/) {
         return false;
     }
     g_stream = g_own_stream;
+    if (g_device >= 0 && g_device < kMaxDevices && !g_scratch[g_device]) {
+        void* sp = nullptr;
+        const hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (se == hipSuccess) {
+            g_scratch[g_device] = static_cast<float*>(sp);
+        } else {
+            (void)hipGetLastError();  // the other entry points do not need it
+            set_error("hipGetSymbolAddress(scratch)", se);
+        }
+    }
     g_initialized = true;
     return true;
 }
@@ -401,6 +447,34 @@ int m4_bridge_validate_gemm(const void* X, size_t Xb, const void* W, size_t Wb, 
 int m4_bridge_dispatch_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format, uint32_t M,
                             uint32_t K, uint32_t N) {
     return gemm_common(X, Xb, W, Wb, Y, Yb, nullptr, format, M, K, N, 0, false);
+}
+
+int m4_bridge_dispatch_gemm_noalloc(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format,
+                                    uint32_t M, uint32_t K, uint32_t N) {
+    if (!g_initialized) return -1;
+    int rc = validate(X, Xb, W, Wb, Y, Yb, format, M, K, N);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    float* ws = (g_device >= 0 && g_device < kMaxDevices) ? g_scratch[g_device] : nullptr;
+    if (!ws) {
+        g_last_error = "no-allocation scratch unavailable on this device";
+        return -6;
+    }
+    // no staging (it would allocate): device buffers only, X and W 16-byte aligned
+    if (device_view(X) != X || device_view(W) != W || device_view(Y) != Y ||
+        (reinterpret_cast<uintptr_t>(X) % 16) || (reinterpret_cast<uintptr_t>(W) % 16)) {
+        g_last_error = "no-allocation projection: X, W and Y must be device memory, X and W 16-byte aligned";
+        return -2;
+    }
+    const size_t wbytes = qr::kernel_weight_bytes(format, K, N);
+    qr::GemmParams p{};
+    p.format = format;
+    p.X = static_cast<const _Float16*>(X);
+    p.W = static_cast<const uint8_t*>(W);
+    p.Y = static_cast<_Float16*>(Y);
+    p.M = M; p.N = N; p.K = K;
+    p.col_bytes = wbytes / N;
+    return launch_ws(p, ws, kScratchFloats);
 }
 
 int m4_bridge_dispatch_router_gemm(void* X, size_t Xb, void* W, size_t Wb, void* Y, size_t Yb, int format,

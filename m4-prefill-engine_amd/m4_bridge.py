@@ -62,6 +62,7 @@ SIGNATURES = {
     "m4_bridge_is_initialized": ([], ctypes.c_bool),
     "m4_bridge_shutdown": ([], None),
     "m4_bridge_validate_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
+    "m4_bridge_dispatch_gemm_noalloc": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_router_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_head_gemm": ([_VP, _SZ, _VP, _SZ, _VP, _SZ, _I, _U32, _U32, _U32, _U32], _I),
     "m4_bridge_dispatch_router_kernel": ([ctypes.c_char_p, _VP, _SZ, _VP, _SZ, _VP, _SZ,
