@@ -126,7 +126,8 @@ def bench_projection(b, timer, name, fmt, M, K, N, seed):
 
     Xn = synth.activations(M, K, seed)
     X = torch.from_numpy(Xn).cuda()
-    Wn = synth.quantized_weights(fmt, N, K, seed + 1) if fmt < 4 else synth.random_blocks(fmt, N, K, seed + 1)
+    Wn = (synth.quantized_weights(fmt, N, K, seed + 1) if fmt < 4 or fmt == synth.MLX_4BIT_G64
+          else synth.random_blocks(fmt, N, K, seed + 1))
     W0 = torch.from_numpy(Wn).cuda()
     Ws = rotated(W0, W0.numel())
     Y = torch.empty(M, N, dtype=torch.float16, device="cuda")
@@ -135,8 +136,11 @@ def bench_projection(b, timer, name, fmt, M, K, N, seed):
     wps = [w.data_ptr() for w in Ws]
     wb = W0.numel()
 
+    # formats beyond the reference's 0..5 go through the kernel-name entry point
+    fn = lib.m4_bridge_dispatch_gemm if fmt < 6 else lib.m4_bridge_dispatch_router_gemm
+
     def step(i):
-        check(lib.m4_bridge_dispatch_gemm(xp, xb, wps[i % len(wps)], wb, yp, yb, fmt, M, K, N), name)
+        check(fn(xp, xb, wps[i % len(wps)], wb, yp, yb, fmt, M, K, N), name)
 
     ms = timer.run(step)
     flops = 2.0 * M * N * K
@@ -428,6 +432,8 @@ def main():
     head_inputs = None
     if on("cfg2_mlx_m128"):
         per["cfg2_mlx_m128"], head_inputs = bench_projection(b, timer, "cfg2_mlx_m128", 1, 128, 4096, 14336, 20)
+    if on("cfg2_mlx_g64_m128"):
+        per["cfg2_mlx_g64_m128"], _ = bench_projection(b, timer, "cfg2_mlx_g64_m128", 8, 128, 4096, 14336, 20)
     if on("cfg1_q4_0_m33"):
         per["cfg1_q4_0_m33"], _ = bench_projection(b, timer, "cfg1_q4_0_m33", 0, 33, 4096, 4096, 10)
     if on("cfg3_q4_k_m2048"):

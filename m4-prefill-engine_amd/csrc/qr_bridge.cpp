@@ -249,9 +249,9 @@ void sync_and_release() {
 
 // Formats m4_bridge_dispatch_gemm accepts (m4_mlx_bridge.mm:28-35, 211), and
 // the wider set the kernel-name entry points accept: every format with a
-// kernel here, i.e. also Q8_0 weights (6) and PRISM_Q2_0 (7).
+// kernel here, i.e. also Q8_0 weights (6), PRISM_Q2_0 (7) and MLX g64 (8).
 bool is_projection_format(int f) { return f >= 0 && f < 6; }
-bool has_kernels(int f) { return f >= 0 && f < 8; }
+bool has_kernels(int f) { return f >= 0 && f <= qr::QUANT_MLX_4BIT_G64; }
 
 // core/bridge/m4_mlx_bridge.mm:204-230, minus the init check.  `ext` widens
 // the format range to every format with kernels (PRISM_Q2_0 needs K % 128).
@@ -264,6 +264,7 @@ int validate(const void* X, size_t Xb, const void* W, size_t Wb, const void* Y, 
     if (K % 32) return -4;
     if ((format == 2 || format == 4 || format == 5) && (K % 256)) return -4;
     if (format == 7 && (K % 128)) return -4;
+    if (format == qr::QUANT_MLX_4BIT_G64 && (K % 64)) return -4;
     if (Xb < (size_t)M * K * 2 || Yb < (size_t)M * N * 2 || Wb < qr::kernel_weight_bytes(format, K, N))
         return -2;
     return 0;
@@ -621,6 +622,7 @@ int m4_bridge_dequantize(void* W, size_t Wb, void* out, size_t outb, int format,
     if (K == 0 || N == 0 || K % 32) return -4;
     if ((format == 2 || format == 4 || format == 5) && K % 256) return -4;
     if (format == 7 && K % 128) return -4;
+    if (format == qr::QUANT_MLX_4BIT_G64 && K % 64) return -4;
     const size_t wbytes = qr::kernel_weight_bytes(format, K, N);
     if (Wb < wbytes || outb < (size_t)N * K * 2) return -2;
     if (wbytes >= (1ull << 31)) return -4;

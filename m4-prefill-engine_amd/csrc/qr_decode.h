@@ -439,6 +439,48 @@ template <> struct Decoder<QUANT_Q8_0> {
     __device__ static uint32_t parity(uint32_t col_off, uint32_t kb) { return (col_off + kb * 34u) & 2u; }
 };
 
+// --------------------------------------------------------------------------
+// MLX_4BIT_G64: 36-byte blocks of 64 elements (dword aligned): fp16 scale and
+// bias, then eight code words, element 8j + i in bits 4i of word j (MLX's
+// packing).  Decode group kb = half kb % 2 of block kb / 2, i.e. code words
+// 4 (kb % 2) .. + 3; w = fma(q, scale, bias) in binary16, one rounding, as
+// MLX_4BIT.  A code word's low and high nibbles are split into two byte
+// vectors and interleaved back into element order with two byte permutes.
+// --------------------------------------------------------------------------
+template <> struct Decoder<QUANT_MLX_4BIT_G64> {
+    static constexpr int kBlockElems = 32;  // decode granularity (half block)
+    static constexpr int kBlockBytes = 36;  // per 64 elements
+    static constexpr int kRawWords = 5;
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t col_off, uint32_t kb, uint32_t raw[5]) {
+        const uint32_t o = col_off + (kb >> 1) * 36u;
+        raw[0] = ld_b32(r, o);
+        const uint32_t c = o + 4u + 16u * (kb & 1u);
+#pragma unroll
+        for (int i = 0; i < 4; i++) raw[i + 1] = ld_b32(r, c + 4u * i);
+    }
+    // bytes {c0, c1, c2, c3} and {c4, c5, c6, c7} of code word w
+    __device__ static void codes8(uint32_t w, uint32_t& a, uint32_t& b) {
+        const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+        a = perm(hi, lo, 0x05010400u);
+        b = perm(hi, lo, 0x07030602u);
+    }
+    __device__ static void decode_half(const uint32_t raw[5], uint32_t, int h, uint32_t out[8]) {
+        const uint32_t d16 = raw[0] & 0xffffu, b16 = raw[0] >> 16;
+        const h2_t d = as_h2(d16 | (d16 << 16));
+        const h2_t bias = as_h2(b16 | (b16 << 16));
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            uint32_t a, b;
+            codes8(raw[1 + 2 * h + i], a, b);
+            out[4 * i + 0] = as_u32(__builtin_elementwise_fma(code_pair<false>(a), d, bias));
+            out[4 * i + 1] = as_u32(__builtin_elementwise_fma(code_pair<true>(a), d, bias));
+            out[4 * i + 2] = as_u32(__builtin_elementwise_fma(code_pair<false>(b), d, bias));
+            out[4 * i + 3] = as_u32(__builtin_elementwise_fma(code_pair<true>(b), d, bias));
+        }
+    }
+    __device__ static uint32_t parity(uint32_t, uint32_t) { return 0; }
+};
+
 // Branch-free half-group decode for pipelined callers: bit-exact whenever no
 // lane of the wave has needs_exact() true for its group (Q4_K and Q4_0 have a
 // slow path; callers check and re-decode with decode_group otherwise).

@@ -41,6 +41,7 @@ hipError_t launch_dequant(int format, const uint8_t* W, _Float16* out, uint32_t 
         case QUANT_EXL3: hipLaunchKernelGGL(dequant_kernel<QUANT_EXL3>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
         case QUANT_Q8_0: hipLaunchKernelGGL(dequant_kernel<QUANT_Q8_0>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
         case QUANT_PRISM_Q2_0: hipLaunchKernelGGL(dequant_kernel<QUANT_PRISM_Q2_0>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
+        case QUANT_MLX_4BIT_G64: hipLaunchKernelGGL(dequant_kernel<QUANT_MLX_4BIT_G64>, grid, dim3(256), 0, st, W, out, K, N, (uint32_t)col_bytes); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

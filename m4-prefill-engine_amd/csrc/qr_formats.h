@@ -21,6 +21,13 @@ enum QuantFormat : int {
     QUANT_EXL3 = 5,
     QUANT_Q8_0 = 6,
     QUANT_PRISM_Q2_0 = 7,
+    // MLX's own 4-bit quantization, groups of 64 (mlx.core.quantize with
+    // group_size 64, bits 4): one 36-byte block per group = the group's fp16
+    // scale and bias followed by its eight uint32 code words exactly as MLX
+    // packs them (element 8j + i in bits 4i of word j).  Not in the
+    // reference, whose MLX_4BIT block is 32 elements (quant_router.h:41-45);
+    // BASELINE's MLX configuration is this layout (4.5 bits per weight).
+    QUANT_MLX_4BIT_G64 = 8,
     QUANT_CUSTOM = 99,
 };
 
@@ -41,6 +48,7 @@ struct block_exl3 {
 };
 struct block_q8_0 { uint16_t d; int8_t qs[32]; };
 struct block_prism_q2_0 { uint16_t d; uint8_t qs[32]; };
+struct block_mlx_4bit_g64 { uint16_t scale; uint16_t bias; uint32_t qs[8]; };
 
 static_assert(sizeof(block_q4_0) == 18, "Q4_0 block is 18 bytes");
 static_assert(sizeof(block_mlx_4bit) == 20, "MLX_4BIT block is 20 bytes");
@@ -50,6 +58,7 @@ static_assert(sizeof(block_var_rate_affine) == 160, "VAR_RATE super-block is 160
 static_assert(sizeof(block_exl3) == 144, "EXL3 super-block is 144 bytes");
 static_assert(sizeof(block_q8_0) == 34, "Q8_0 block is 34 bytes");
 static_assert(sizeof(block_prism_q2_0) == 34, "PRISM_Q2_0 block is 34 bytes");
+static_assert(sizeof(block_mlx_4bit_g64) == 36, "MLX_4BIT_G64 block is 36 bytes");
 
 struct QuantFormatInfo {
     QuantFormat format;
@@ -71,6 +80,7 @@ inline QuantFormatInfo get_quant_info(QuantFormat fmt) {
         case QUANT_EXL3: return {fmt, "EXL3", "ExLlamaV3 256-elem hierarchical vector codebook super-block with residual correction", 256, 144, 4.50};
         case QUANT_Q8_0: return {fmt, "Q8_0", "Standard 32-elem 8-bit symmetric block (FP16 scale)", 32, 34, 8.50};
         case QUANT_PRISM_Q2_0: return {fmt, "PRISM_Q2_0", "PrismML Q2_0 128-elem ternary {-1, 0, +1} block (FP16 scale)", 128, 34, 2.125};
+        case QUANT_MLX_4BIT_G64: return {fmt, "MLX_4BIT_G64", "MLX 64-elem affine group (FP16 scale + FP16 bias, 8 codes per uint32)", 64, 36, 4.50};
         default: break;
     }
     return {QUANT_Q4_0, "UNKNOWN", "Unknown format", 32, 0, 0.0};
@@ -100,11 +110,13 @@ inline size_t expected_weight_bytes(int format, uint32_t K, uint32_t N) {
 // W bytes the kernels read for every format that has kernels here: formats
 // 0..5 as above, plus Q8_0 weights (34 B / 32) and PRISM_Q2_0 (34 B / 128),
 // which the reference reaches only through its kernel names
-// (quant_router_kernels.metal:726, :904; quant_registry.mm:153).
+// (quant_router_kernels.metal:726, :904; quant_registry.mm:153), and MLX's
+// native g64 groups (36 B / 64).
 inline size_t kernel_weight_bytes(int format, uint32_t K, uint32_t N) {
     switch (format) {
         case QUANT_Q8_0: return ((size_t)K / 32) * N * 34;
         case QUANT_PRISM_Q2_0: return ((size_t)K / 128) * N * 34;
+        case QUANT_MLX_4BIT_G64: return ((size_t)K / 64) * N * 36;
         default: return expected_weight_bytes(format, K, N);
     }
 }

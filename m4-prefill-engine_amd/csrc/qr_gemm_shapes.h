@@ -60,7 +60,7 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     // for the formats with a cheap decode (measured at M = 129: Q4_0, MLX and
     // ternary 6-20% faster, Q4_K 8-9% slower)
     const bool cheap = format == QUANT_Q4_0 || format == QUANT_MLX_4BIT || format == QUANT_TERNARY_1_58 ||
-                       format == QUANT_Q8_0 || format == QUANT_PRISM_Q2_0;
+                       format == QUANT_Q8_0 || format == QUANT_PRISM_Q2_0 || format == QUANT_MLX_4BIT_G64;
     const uint32_t tail = M % 128;
 #ifdef QR_RB_MID64_FILL
     // 64-row tiles whenever 128-row tiles leave the CUs under-filled

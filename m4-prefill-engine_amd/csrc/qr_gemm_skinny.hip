@@ -162,6 +162,30 @@ template <> struct Frag<QUANT_TERNARY_1_58> {
 };
 
 
+// MLX_4BIT_G64 (36-byte 64-element blocks): group kb is half kb % 2 of block
+// kb / 2; lane group g takes code word 4 (kb % 2) + g, i.e. elements
+// 8g .. 8g + 7 of the group, in element order (two byte permutes).
+template <> struct Frag<QUANT_MLX_4BIT_G64> {
+    static constexpr bool kNibbleOrder = false;
+    static constexpr int kRaw = 2;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
+        const uint8_t* p = strip + (kb >> 1) * 36u;
+        raw[0] = lds32(p);
+        raw[1] = lds32(p + 4u + 16u * (kb & 1u) + 4u * (uint32_t)g);
+    }
+    __device__ static h8_t decode(const uint32_t raw[2], uint32_t, int) {
+        const uint32_t d16 = raw[0] & 0xffffu, b16 = raw[0] >> 16;
+        const h2_t d = as_h2(d16 | (d16 << 16)), bias = as_h2(b16 | (b16 << 16));
+        const uint32_t lo = raw[1] & 0x0f0f0f0fu, hi = (raw[1] >> 4) & 0x0f0f0f0fu;
+        const uint32_t a = perm(hi, lo, 0x05010400u), b = perm(hi, lo, 0x07030602u);
+        u4_t w = {as_u32(__builtin_elementwise_fma(code_pair<false>(a), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<true>(a), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<false>(b), d, bias)),
+                  as_u32(__builtin_elementwise_fma(code_pair<true>(b), d, bias))};
+        return __builtin_bit_cast(h8_t, w);
+    }
+};
+
 constexpr int kSkWaves = 8;
 constexpr int kSkNT = 4;                  // 16-column tiles per wave
 constexpr int kSkCols = 16 * kSkNT;       // columns per workgroup
@@ -173,6 +197,7 @@ template <> struct GroupBytes<QUANT_Q4_0> { static constexpr uint32_t v = 18; };
 template <> struct GroupBytes<QUANT_MLX_4BIT> { static constexpr uint32_t v = 20; };
 template <> struct GroupBytes<QUANT_Q4_K> { static constexpr uint32_t v = 18; };  // 144 / 8
 template <> struct GroupBytes<QUANT_TERNARY_1_58> { static constexpr uint32_t v = 12; };
+template <> struct GroupBytes<QUANT_MLX_4BIT_G64> { static constexpr uint32_t v = 18; };  // 36 / 2
 
 // LDS layout of one launch: activation rows [M][KC*2 + 16 bytes], then 64
 // weight strips [64][SB + 16 bytes]; the wave reduction reuses it from 0.
@@ -348,6 +373,7 @@ static uint32_t group_bytes_rt(int f) {
         case QUANT_MLX_4BIT: return GroupBytes<QUANT_MLX_4BIT>::v;
         case QUANT_Q4_K: return GroupBytes<QUANT_Q4_K>::v;
         case QUANT_TERNARY_1_58: return GroupBytes<QUANT_TERNARY_1_58>::v;
+        case QUANT_MLX_4BIT_G64: return GroupBytes<QUANT_MLX_4BIT_G64>::v;
         default: return 0;
     }
 }
@@ -375,7 +401,7 @@ static bool sk_plan(int f, uint32_t M, uint32_t N, uint32_t K, uint32_t* ks_out,
 
 size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K) {
     uint32_t ks_max = 1;
-    for (int f = 0; f < 4; f++) {
+    for (int f : {0, 1, 2, 3, (int)QUANT_MLX_4BIT_G64}) {
         uint32_t ks = 1, gpw = 1;
         if (sk_plan(f, M, N, K, &ks, &gpw) && ks > ks_max) ks_max = ks;
     }
@@ -423,7 +449,7 @@ static hipError_t launch_sk_m(const GemmParams& p, float* ws, hipStream_t st) {
 }
 
 bool skinny_supported(const GemmParams& p) {
-    if (p.W2 || p.format < 0 || p.format > 3) return false;
+    if (p.W2 || !((p.format >= 0 && p.format <= 3) || p.format == QUANT_MLX_4BIT_G64)) return false;
     if (p.col_bytes % 16) return false;
     uint32_t ks, gpw;
     return sk_plan(p.format, p.M, p.N, p.K, &ks, &gpw);
@@ -435,6 +461,7 @@ hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, hipStream_t st) {
         case QUANT_MLX_4BIT: return launch_sk_m<QUANT_MLX_4BIT>(p, ws, st);
         case QUANT_Q4_K: return launch_sk_m<QUANT_Q4_K>(p, ws, st);
         case QUANT_TERNARY_1_58: return launch_sk_m<QUANT_TERNARY_1_58>(p, ws, st);
+        case QUANT_MLX_4BIT_G64: return launch_sk_m<QUANT_MLX_4BIT_G64>(p, ws, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -69,6 +69,8 @@ void QuantRegistry::register_builtin_codecs() {
         {QUANT_EXL3, "ExLlamaV3 256-elem super-block with vector codebook", "exl3"},
         {QUANT_Q8_0, "Standard GGUF Q8_0 Symmetric 32-element blocks (for KV cache)", "q8_0"},
         {QUANT_PRISM_Q2_0, "PrismML Q2_0 128-elem ternary {-1, 0, +1} block (FP16 scale)", "prism_q2_0"},
+        // not registered by the reference: MLX's native 64-element groups
+        {QUANT_MLX_4BIT_G64, "MLX 4-bit affine, native 64-element groups (8 codes per uint32)", "mlx_4bit_g64"},
     };
     for (const auto& r : rows) {
         QuantFormatInfo info = get_quant_info(r.f);

@@ -25,6 +25,10 @@ class QuantFormat(IntEnum):
     QUANT_TERNARY_1_58 = 3
     QUANT_VAR_RATE_AFFINE = 4
     QUANT_EXL3 = 5
+    # beyond the reference's dispatchable range (kernel-name entry points only)
+    QUANT_Q8_0 = 6
+    QUANT_PRISM_Q2_0 = 7
+    QUANT_MLX_4BIT_G64 = 8  # MLX's native 64-element groups (36 B / 64)
 
 
 LIB_NAME = "libm4_bridge.so"

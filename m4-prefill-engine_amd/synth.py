@@ -21,8 +21,9 @@ import numpy as np
 
 Q4_0, MLX_4BIT, Q4_K, TERNARY_1_58, VAR_RATE_AFFINE, EXL3 = 0, 1, 2, 3, 4, 5
 Q8_0, PRISM_Q2_0 = 6, 7
-BLOCK_ELEMS = {0: 32, 1: 32, 2: 256, 3: 32, 4: 256, 5: 256, 6: 32, 7: 128}
-BLOCK_BYTES = {0: 18, 1: 20, 2: 144, 3: 12, 4: 160, 5: 144, 6: 34, 7: 34}
+MLX_4BIT_G64 = 8  # MLX's native 64-element groups (not a reference format)
+BLOCK_ELEMS = {0: 32, 1: 32, 2: 256, 3: 32, 4: 256, 5: 256, 6: 32, 7: 128, 8: 64}
+BLOCK_BYTES = {0: 18, 1: 20, 2: 144, 3: 12, 4: 160, 5: 144, 6: 34, 7: 34, 8: 36}
 
 
 def _h16_bytes(x: np.ndarray) -> np.ndarray:
@@ -108,6 +109,22 @@ def quantize_mlx_4bit(w: np.ndarray) -> np.ndarray:
     return mlx_g64_to_router_blocks(*quantize_mlx_g64(w))
 
 
+def mlx_g64_blocks(scale: np.ndarray, bias: np.ndarray, packed: np.ndarray) -> np.ndarray:
+    """MLX g64 arrays (scales / biases fp16 [N, K/64], packed uint32 [N, K/8])
+    -> MLX_4BIT_G64 blocks: per group its scale, bias and eight code words,
+    unchanged (36 bytes per 64 weights)."""
+    N, G = scale.shape
+    out = np.empty((N, G, 36), np.uint8)
+    out[..., 0:2] = np.ascontiguousarray(scale, np.float16).view(np.uint8).reshape(N, G, 2)
+    out[..., 2:4] = np.ascontiguousarray(bias, np.float16).view(np.uint8).reshape(N, G, 2)
+    out[..., 4:] = np.ascontiguousarray(packed, np.uint32).reshape(N, G, 8).view(np.uint8)
+    return out.reshape(-1)
+
+
+def quantize_mlx_4bit_g64(w: np.ndarray) -> np.ndarray:
+    return mlx_g64_blocks(*quantize_mlx_g64(w))
+
+
 def _pack_q4k_scales(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
     """sc, mn [..., 8] 6-bit -> scales[12] in the reference's packing
     (bench_universal_router.mm:70-78; decoded at cpu_gold_reference.h:121-127)."""
@@ -183,6 +200,8 @@ def quantized_weights(fmt: int, N: int, K: int, seed: int, std: float = 0.02) ->
         return quantize_q4_0(w)
     if fmt == MLX_4BIT:
         return quantize_mlx_4bit(w)
+    if fmt == MLX_4BIT_G64:
+        return quantize_mlx_4bit_g64(w)
     if fmt == Q4_K:
         return quantize_q4_k(w)
     raise ValueError(f"no quantizer for format {fmt}")
@@ -228,6 +247,12 @@ def random_blocks(fmt: int, N: int, K: int, seed: int, code3: bool = False) -> n
         out = np.empty((N, nb, 34), np.uint8)
         out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.004 + 0.0005).astype(np.float32))
         out[..., 2:] = rng.integers(0, 256, (N, nb, 32), dtype=np.uint8)
+    elif fmt == MLX_4BIT_G64:
+        # MLX_4BIT's reference ranges (d in [0.001, 0.031), bias in [-0.05, 0.05)), one per 64
+        out = np.empty((N, nb, 36), np.uint8)
+        out[..., 0:2] = _h16_bytes((rng.random((N, nb)) * 0.03 + 0.001).astype(np.float32))
+        out[..., 2:4] = _h16_bytes((rng.random((N, nb)) * 0.1 - 0.05).astype(np.float32))
+        out[..., 4:] = rng.integers(0, 256, (N, nb, 32), dtype=np.uint8)
     elif fmt == PRISM_Q2_0:
         # tests/e2e/test_common.h:415-427: d in [0.01, 0.05), every 2-bit code
         # 0..3 (code 3 included), four per byte LSB first

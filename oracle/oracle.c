@@ -27,6 +27,7 @@
  *                        i8 codebook[16] | u8 pad[12] | u8 qs[96]
  *   Q8_0     34 B / 32: f16 d | i8 qs[32]
  *   PRISM    34 B / 128: f16 d | u8 qs[32]
+ *   MLX_G64  36 B / 64: f16 scale | f16 bias | u32 qs[8]  (MLX's own layout)
  *
  * Parity pins for each function are listed in tests/test_oracle.py.
  */
@@ -97,13 +98,14 @@ static inline uint16_t f32_to_f16(float x) { return orc_f64_to_f16((double)x); }
 /* Format table (quant_router.h:110-136; core/bridge/m4_mlx_bridge.mm:58-75) */
 /* ------------------------------------------------------------------------ */
 
-enum { F_Q4_0 = 0, F_MLX = 1, F_Q4_K = 2, F_TERN = 3, F_VAR = 4, F_EXL3 = 5, F_Q8_0 = 6, F_PRISM = 7 };
+enum { F_Q4_0 = 0, F_MLX = 1, F_Q4_K = 2, F_TERN = 3, F_VAR = 4, F_EXL3 = 5, F_Q8_0 = 6, F_PRISM = 7, F_G64 = 8 };
+#define F_LAST F_G64
 
-static const uint32_t kBlockElems[8] = {32, 32, 256, 32, 256, 256, 32, 128};
-static const uint32_t kBlockBytes[8] = {18, 20, 144, 12, 160, 144, 34, 34};
+static const uint32_t kBlockElems[9] = {32, 32, 256, 32, 256, 256, 32, 128, 64};
+static const uint32_t kBlockBytes[9] = {18, 20, 144, 12, 160, 144, 34, 34, 36};
 
-EXPORT uint32_t orc_block_elems(int f) { return (f >= 0 && f < 8) ? kBlockElems[f] : 0; }
-EXPORT uint32_t orc_block_bytes(int f) { return (f >= 0 && f < 8) ? kBlockBytes[f] : 0; }
+EXPORT uint32_t orc_block_elems(int f) { return (f >= 0 && f <= F_LAST) ? kBlockElems[f] : 0; }
+EXPORT uint32_t orc_block_bytes(int f) { return (f >= 0 && f <= F_LAST) ? kBlockBytes[f] : 0; }
 
 /*
  * Exact weights of ONE block, in element order, as doubles, plus the order in
@@ -256,6 +258,17 @@ static void dec_prism(const uint8_t* b, double w[128]) {
         for (int j = 0; j < 4; j++) w[i * 4 + j] = (double)((int)((b[2 + i] >> (2 * j)) & 3) - 1) * d;
 }
 
+/* MLX_4BIT_G64 (not a reference format): MLX's affine dequantization of one
+ * 64-element group, w = scale * q + bias (mlx.core.dequantize, bits 4,
+ * group_size 64), element 8j + i at bits 4i of little-endian code word j. */
+static void dec_g64(const uint8_t* b, double w[64]) {
+    double scale = hf(b), bias = hf(b + 2);
+    for (int j = 0; j < 8; j++) {
+        uint32_t word = rd32(b + 4 + 4 * j);
+        for (int i = 0; i < 8; i++) w[8 * j + i] = (double)((word >> (4 * i)) & 15u) * scale + bias;
+    }
+}
+
 static void decode_block(int f, const uint8_t* b, double* w) {
     switch (f) {
         case F_Q4_0: dec_q4_0(b, w); break;
@@ -266,13 +279,14 @@ static void decode_block(int f, const uint8_t* b, double* w) {
         case F_EXL3: dec_exl3(b, w); break;
         case F_Q8_0: dec_q8_0(b, w); break;
         case F_PRISM: dec_prism(b, w); break;
+        case F_G64: dec_g64(b, w); break;
     }
 }
 
 /* Dequantize a [N, K] weight matrix to fp16 bits with ONE RNE rounding of the
  * exact double value the CPU gold uses (the bit-exact dequant contract). */
 EXPORT int orc_dequantize(int f, const uint8_t* W, uint16_t* out, uint32_t K, uint32_t N) {
-    if (f < 0 || f > 7) return -3;
+    if (f < 0 || f > F_LAST) return -3;
     uint32_t bs = kBlockElems[f], bb = kBlockBytes[f];
     if (K % bs) return -4;
     uint32_t nb = K / bs;
@@ -287,7 +301,7 @@ EXPORT int orc_dequantize(int f, const uint8_t* W, uint16_t* out, uint32_t K, ui
 
 /* Same, as the exact doubles (no rounding). */
 EXPORT int orc_dequantize_f64(int f, const uint8_t* W, double* out, uint32_t K, uint32_t N) {
-    if (f < 0 || f > 7) return -3;
+    if (f < 0 || f > F_LAST) return -3;
     uint32_t bs = kBlockElems[f], bb = kBlockBytes[f];
     if (K % bs) return -4;
     uint32_t nb = K / bs;
@@ -395,7 +409,7 @@ static void gemm_row(void* vctx, size_t m) {
 EXPORT int orc_gemm(int f, const uint16_t* A, const uint8_t* B, uint16_t* C, const uint16_t* R,
                     uint32_t M, uint32_t N, uint32_t K, int direct_head, uint32_t H, uint32_t D,
                     int nthreads) {
-    if (f < 0 || f > 7) return -3;
+    if (f < 0 || f > F_LAST) return -3;
     if (K % kBlockElems[f]) return -4;
     gemm_ctx c = {f, A, B, C, R, M, N, K, H, D, direct_head, NULL};
     parallel_rows(gemm_row, &c, M, nthreads);
@@ -433,7 +447,7 @@ static void swiglu_row(void* vctx, size_t m) {
 
 EXPORT int orc_swiglu(int f, const uint16_t* A, const uint8_t* Bg, const uint8_t* Bu, uint16_t* O,
                       uint32_t M, uint32_t N, uint32_t K, int nthreads) {
-    if (f < 0 || f > 7) return -3;
+    if (f < 0 || f > F_LAST) return -3;
     if (K % kBlockElems[f]) return -4;
     swiglu_ctx c = {f, A, Bg, Bu, O, M, N, K};
     parallel_rows(swiglu_row, &c, M, nthreads);

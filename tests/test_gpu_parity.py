@@ -54,13 +54,13 @@ def weights(kind, fmt, N, K, seed):
 # --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("fmt,K", [(0, 512), (0, 96), (1, 512), (1, 96), (2, 512), (3, 512), (3, 96), (4, 512),
-                                   (5, 512), (6, 512), (6, 96), (7, 512), (7, 384)])
+                                   (5, 512), (6, 512), (6, 96), (7, 512), (7, 384), (8, 512), (8, 192)])
 @pytest.mark.parametrize("kind", ["random", "quantized"])
 def test_dequant_bit_exact(bridge, oracle, fmt, K, kind):
     N = 72
     if kind == "quantized" and fmt == 1 and K % 64:
         pytest.skip("MLX g64 quantizer needs K % 64 == 0")
-    if kind == "quantized" and fmt >= 4:
+    if kind == "quantized" and 4 <= fmt <= 7:
         pytest.skip("formats 4..7 come from random generators only (no BASELINE quantizer)")
     W = weights(kind, fmt, N, K, 100 + fmt)
     out = empty16(N, K)
@@ -435,7 +435,7 @@ def test_direct_head_and_residual(bridge, oracle, fmt):
 # SwiGLU
 # --------------------------------------------------------------------------
 
-@pytest.mark.parametrize("fmt", [0, 1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("M", [33, 128, 129])
 def test_swiglu(bridge, oracle, fmt, M):
     # brick3_swiglu_bench.mm:268-426 verifies M in {33,127,128,129}
@@ -821,3 +821,47 @@ def torch_empty_u8(n):
     import torch
 
     return torch.empty(n, dtype=torch.uint8, device="cuda")
+
+
+# --------------------------------------------------------------------------
+# MLX_4BIT_G64 (format 8): MLX's native 64-element groups
+# --------------------------------------------------------------------------
+
+def test_mlx_g64_decode_equals_router_repack(bridge):
+    """The native g64 decoder and the MLX_4BIT decoder of the lossless
+    g64 -> 32-element repack give the same binary16 weights, bit for bit."""
+    N, K = 96, 1024
+    scale, bias, packed = synth.quantize_mlx_g64(synth.gaussian_weights(N, K, 401))
+    Wg = synth.mlx_g64_blocks(scale, bias, packed)
+    Wr = synth.mlx_g64_to_router_blocks(scale, bias, packed)
+    a, b = empty16(N, K), empty16(N, K)
+    bridge.dequantize(dev(Wg), a, 8, K, N)
+    bridge.dequantize(dev(Wr), b, 1, K, N)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(a).view(np.uint16), host(b).view(np.uint16))
+
+
+@pytest.mark.parametrize("M", [1, 16, 33, 64, 127, 128, 129, 300, 2048])
+@pytest.mark.parametrize("kind", ["random", "quantized"])
+def test_mlx_g64_projection(bridge, oracle, M, kind):
+    """Small-M (M <= 64, K split) and tiled kernels, standard, residual and
+    direct-head outputs, on reference-style random groups and on N(0, 0.02)
+    weights quantized by MLX's rule."""
+    K, N = (512, 256) if M in (127, 2048) else (2048, 320)
+    std = 0.35 if kind == "random" else 1.0
+    X = synth.activations(M, K, 410 + M, std=std)
+    W = weights(kind, 8, N, K, 411 + M)
+    Y = empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, 8, M, K, N)
+    R = synth.activations(M, N, 412)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, 8, M, K, N)
+    H, D = N // 64, 64
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, 8, M, H, D, K)
+    with pytest.raises(RuntimeError):  # the reference's projection entry point keeps formats 0..5
+        bridge.dispatch_gemm(dev(X), dev(W), empty16(M, N), 8, M, K, N)
+    bridge.synchronize()
+    tolerance.check_ref(host(Y), oracle.gemm(8, X, W, N), what=f"g64 {kind} M={M}")
+    tolerance.check_ref(host(Yr), oracle.gemm(8, X, W, N, R=R), what="g64 residual")
+    tolerance.check_ref(host(Yh), oracle.gemm(8, X, W, N, head_D=D), what="g64 direct-head")

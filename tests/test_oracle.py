@@ -560,3 +560,26 @@ def test_row_sampled_attention_and_layer_equal_the_full_ones(oracle):
     full = oracle.layer(0, X, *Wl, H=Hq, D=D, N_mlp=Nm, scale=0.17)
     r = oracle.layer_ex_rows(0, X, None, *Wl[:4], None, *Wl[4:], pos, Hq=Hq, Hkv=Hq, D=D, N_mlp=Nm, scale=0.17)
     np.testing.assert_array_equal(r, full[pos])
+
+
+def test_mlx_g64_block_known_answers(oracle):
+    """MLX_4BIT_G64 blocks: element 8j + i is nibble i of code word j and
+    w = scale * q + bias (mlx.core.dequantize); a layout probe with one
+    nonzero nibble at a time catches swapped words or nibble order, and the
+    block's decode equals the MLX_4BIT decode of the g64 -> router repack."""
+    blk = np.zeros(36, np.uint8)
+    blk[0:2] = np.array([0.25], np.float16).view(np.uint8)
+    blk[2:4] = np.array([-1.0], np.float16).view(np.uint8)
+    for j in range(8):
+        for i in range(8):
+            b = blk.copy()
+            words = np.zeros(8, np.uint32)
+            words[j] = np.uint32(15) << np.uint32(4 * i)
+            b[4:] = words.view(np.uint8)
+            w = oracle.dequantize_f64(8, b, 64, 1)[0]
+            expect = np.full(64, -1.0)
+            expect[8 * j + i] = 15 * 0.25 - 1.0
+            np.testing.assert_array_equal(w, expect)
+    scale, bias, packed = synth.quantize_mlx_g64(synth.gaussian_weights(8, 256, 9))
+    np.testing.assert_array_equal(oracle.dequantize_f64(8, synth.mlx_g64_blocks(scale, bias, packed), 256, 8),
+                                  oracle.dequantize_f64(1, synth.mlx_g64_to_router_blocks(scale, bias, packed), 256, 8))
