@@ -189,6 +189,17 @@ M4_API int m4_bridge_prefill_layer_ex(void* X_ptr, void* w_attn, void* Wq, void*
                                uint32_t N_mlp, float attn_scale, int norm_type, float norm_eps, int rope,
                                float rope_theta, uint32_t rope_offset, int rope_traditional);
 
+/* m4_bridge_prefill_layer_ex that also hands back the layer's Q8_0 KV cache
+ * (the d_K_q8 / d_V_q8 buffers of unified_prefill_engine.mm:548-572): Kq_out
+ * and Vq_out, device memory of Hkv * M * D / 32 * 34 bytes each, receive the
+ * Q8_0 blocks of K and V ([Hkv, M, D], 32 consecutive d per 34-byte block,
+ * K after RoPE).  Both NULL: m4_bridge_prefill_layer_ex; only one: -2. */
+M4_API int m4_bridge_prefill_layer_ex_kv(void* X_ptr, void* w_attn, void* Wq, void* Wk, void* Wv, void* Wo,
+                                  void* w_ffn, void* Wg, void* Wu, void* Wd, void* X_out, void* Kq_out,
+                                  void* Vq_out, int format, uint32_t M, uint32_t d_model, uint32_t Hq, uint32_t Hkv,
+                                  uint32_t D, uint32_t N_mlp, float attn_scale, int norm_type, float norm_eps,
+                                  int rope, float rope_theta, uint32_t rope_offset, int rope_traditional);
+
 /* Dequantize W [N, K] to fp16 [N, K] with the kernels' own decoders (the
  * registry's dequantize hook, src/router/quant_registry.h:24). Formats 0..7. */
 M4_API int m4_bridge_dequantize(void* W_ptr, size_t W_bytes, void* out_ptr, size_t out_bytes, int format,

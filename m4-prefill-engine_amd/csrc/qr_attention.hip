@@ -135,13 +135,14 @@ __device__ __forceinline__ void attn_stage_f16(const AttnRawF16<D>& raw, int tid
 // tile of one head.  FROM_Q8: from Q8_0 blocks (half(q * half(d)), the
 // reference's dequantizer, brick4_attn_bench.mm:57-65); otherwise from fp16
 // K / V through the same quantize-then-dequantize arithmetic as
-// quantize_q8_0_kernel + the Q8_0 path (bit-identical values, no Q8_0 buffer
-// written).  K units (one key's block) write K' rows straight out; V units
+// quantize_q8_0_kernel + the Q8_0 path (bit-identical values), also writing
+// the Q8_0 blocks themselves to Kq / Vq when those are given -- the layer's
+// Q8_0 KV cache, produced in the same pass.  K units (one key's block) write K' rows straight out; V units
 // (a key pair's blocks) write {V[k][d], V[k+1][d]} words into an LDS tile
 // [d][key], whose rows then leave as 128-byte runs of V'^T.  Keys M .. Mp - 1
 // are zero.
 template <bool FROM_Q8>
-__device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t w[16]) {
+__device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t w[16], uint8_t* q8out) {
     uint32_t d16, codes[8];  // code word c: codes of elements 4c .. 4c + 3
     if constexpr (FROM_Q8) {
         // 34-byte blocks are 2-byte aligned.  From the aligned dword at or
@@ -166,6 +167,12 @@ __device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t
         quantize_block_q8_0(x, d16, c16);
 #pragma unroll
         for (int c = 0; c < 8; c++) codes[c] = c16[2 * c] | (c16[2 * c + 1] << 16);
+        if (q8out) {  // 34-byte blocks are 2-byte aligned
+            uint16_t* o16 = reinterpret_cast<uint16_t*>(q8out + blk * 34);
+            o16[0] = (uint16_t)d16;
+#pragma unroll
+            for (int i = 0; i < 16; i++) o16[1 + i] = (uint16_t)c16[i];
+        }
     }
     const h2_t d = as_h2(d16 | (d16 << 16));
 #pragma unroll
@@ -177,7 +184,7 @@ __device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t
 
 template <int D, bool FROM_Q8>
 __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const void* Vsrc, _Float16* Kf, _Float16* Vtf,
-                                                      uint32_t M, uint32_t Mp) {
+                                                      uint8_t* Kq, uint8_t* Vq, uint32_t M, uint32_t Mp) {
     constexpr int NB = D / 32;            // blocks per key
     constexpr int TR = kBKV + 8;          // LDS row (halfs) of the transposed tile
     constexpr int KU = kBKV * NB, VU = (kBKV / 2) * NB;
@@ -190,7 +197,7 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
             const int key = u % kBKV, db = u / kBKV;
             const uint32_t gk = k0 + key;
             uint32_t w[16] = {};
-            if (gk < M) prep_block<FROM_Q8>(Ksrc, hk * head_blocks + (size_t)gk * NB + db, w);
+            if (gk < M) prep_block<FROM_Q8>(Ksrc, hk * head_blocks + (size_t)gk * NB + db, w, Kq);
             u4_t* dst = reinterpret_cast<u4_t*>(Kf + hk * head_dst + (size_t)gk * D + db * 32);
 #pragma unroll
             for (int c = 0; c < 4; c++) dst[c] = u4_t{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
@@ -201,7 +208,7 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const uint32_t gk = k0 + 2 * kp + e;
-                if (gk < M) prep_block<FROM_Q8>(Vsrc, hk * head_blocks + (size_t)gk * NB + db, w[e]);
+                if (gk < M) prep_block<FROM_Q8>(Vsrc, hk * head_blocks + (size_t)gk * NB + db, w[e], Vq);
             }
             uint32_t* t32 = reinterpret_cast<uint32_t*>(T);
 #pragma unroll
@@ -742,14 +749,15 @@ hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
 uint32_t kv_padded_len(uint32_t M) { return (M + kBKV - 1) / kBKV * kBKV; }
 
 hipError_t launch_kv_prep(const void* K, const void* V, bool from_q8, _Float16* Kf, _Float16* Vtf, uint32_t Hkv,
-                          uint32_t M, uint32_t D, hipStream_t st) {
+                          uint32_t M, uint32_t D, hipStream_t st, uint8_t* Kq, uint8_t* Vq) {
     const uint32_t Mp = kv_padded_len(M);
     dim3 grid(Mp / kBKV, Hkv);
+    if (from_q8) Kq = Vq = nullptr;  // the blocks are the input
     switch (D * 2 + (from_q8 ? 1 : 0)) {
-        case 128: hipLaunchKernelGGL((kv_prep_kernel<64, false>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
-        case 129: hipLaunchKernelGGL((kv_prep_kernel<64, true>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
-        case 256: hipLaunchKernelGGL((kv_prep_kernel<128, false>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
-        case 257: hipLaunchKernelGGL((kv_prep_kernel<128, true>), grid, dim3(256), 0, st, K, V, Kf, Vtf, M, Mp); break;
+        case 128: hipLaunchKernelGGL((kv_prep_kernel<64, false>), grid, dim3(256), 0, st, K, V, Kf, Vtf, Kq, Vq, M, Mp); break;
+        case 129: hipLaunchKernelGGL((kv_prep_kernel<64, true>), grid, dim3(256), 0, st, K, V, Kf, Vtf, Kq, Vq, M, Mp); break;
+        case 256: hipLaunchKernelGGL((kv_prep_kernel<128, false>), grid, dim3(256), 0, st, K, V, Kf, Vtf, Kq, Vq, M, Mp); break;
+        case 257: hipLaunchKernelGGL((kv_prep_kernel<128, true>), grid, dim3(256), 0, st, K, V, Kf, Vtf, Kq, Vq, M, Mp); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

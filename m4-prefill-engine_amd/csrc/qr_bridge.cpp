@@ -649,7 +649,21 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
                                void* Wu, void* Wd, void* Xout, int format, uint32_t M, uint32_t dm, uint32_t Hq,
                                uint32_t Hkv, uint32_t D, uint32_t Nm, float scale, int norm_type, float eps,
                                int rope, float theta, uint32_t offset, int traditional) {
+    return m4_bridge_prefill_layer_ex_kv(X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, Xout, nullptr, nullptr, format, M,
+                                         dm, Hq, Hkv, D, Nm, scale, norm_type, eps, rope, theta, offset, traditional);
+}
+
+int m4_bridge_prefill_layer_ex_kv(void* X, void* w_attn, void* Wq, void* Wk, void* Wv, void* Wo, void* w_ffn, void* Wg,
+                                  void* Wu, void* Wd, void* Xout, void* Kq_out, void* Vq_out, int format, uint32_t M,
+                                  uint32_t dm, uint32_t Hq, uint32_t Hkv, uint32_t D, uint32_t Nm, float scale,
+                                  int norm_type, float eps, int rope, float theta, uint32_t offset, int traditional) {
     if (!g_initialized) return -1;
+    if ((Kq_out == nullptr) != (Vq_out == nullptr)) return -2;
+    for (void* q : {Kq_out, Vq_out}) {
+        if (!q) continue;
+        void* d = device_view(q);
+        if (!d || d != q || (reinterpret_cast<uintptr_t>(q) % 2)) return -2;  // device, 2-byte aligned blocks
+    }
     void* ptrs[9] = {X, Wq, Wk, Wv, Wo, Wg, Wu, Wd, Xout};
     for (void* q : ptrs)
         if (!q) return -2;
@@ -671,10 +685,11 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
     std::lock_guard<std::mutex> lk(g_mu);
     const size_t nq = (size_t)M * HQ, nk = (size_t)M * HK;
     const uint32_t Mp = qr::kv_padded_len(M);
-    const size_t kvf = (size_t)Hkv * Mp * D * 2;  // one dequantized fp16 cache (K or V^T)
+    const size_t kvf = (size_t)Hkv * Mp * D * 2;  // one dequantized fp16 working copy (K or V^T)
+    const size_t kvq = nk / 32 * 34;              // the Q8_0 cache of K or V
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     const bool norms = w_attn || w_ffn;
-    const size_t need = 2 * al(nq * 2) + 2 * al(nk * 2) + 2 * al(kvf) + al((size_t)M * dm * 2) +
+    const size_t need = 2 * al(nq * 2) + 2 * al(nk * 2) + 2 * al(kvf) + 2 * al(kvq) + al((size_t)M * dm * 2) +
                         al((size_t)M * Nm * 2) + (norms ? al((size_t)M * dm * 2) : 0);
     if (grow(&g_ws, &g_ws_bytes, need, false, "layer scratch") != hipSuccess) return -5;
     uint8_t* w = static_cast<uint8_t*>(g_ws);
@@ -684,6 +699,12 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
     _Float16* v = reinterpret_cast<_Float16*>(take(nk * 2));
     _Float16* kf = reinterpret_cast<_Float16*>(take(kvf));
     _Float16* vtf = reinterpret_cast<_Float16*>(take(kvf));
+    uint8_t* kq = take(kvq);
+    uint8_t* vq = take(kvq);
+    if (Kq_out) {  // the caller keeps the Q8_0 KV cache
+        kq = static_cast<uint8_t*>(Kq_out);
+        vq = static_cast<uint8_t*>(Vq_out);
+    }
     _Float16* o = reinterpret_cast<_Float16*>(take(nq * 2));
     _Float16* xm = reinterpret_cast<_Float16*>(take((size_t)M * dm * 2));
     _Float16* s = reinterpret_cast<_Float16*>(take((size_t)M * Nm * 2));
@@ -742,9 +763,10 @@ int m4_bridge_prefill_layer_ex(void* X, void* w_attn, void* Wq, void* Wk, void* 
         rc = rc ? rc : check(qr::launch_rope(k, Hkv, M, D, theta, offset, traditional, g_stream), "layer rope");
     }
     if (!rc) {
-        // Q8_0 KV cache (unified_prefill_engine.mm:554-572) as its dequantized
-        // values: quantize + dequantize in registers, fp16 K and V^T out
-        hipError_t e = qr::launch_kv_prep(k, v, false, kf, vtf, Hkv, M, D, g_stream);
+        // The Q8_0 KV cache (unified_prefill_engine.mm:548-572), written in
+        // the same pass that dequantizes it into the attention kernel's fp16
+        // K / V^T working copy (quantize + dequantize in registers).
+        hipError_t e = qr::launch_kv_prep(k, v, false, kf, vtf, Hkv, M, D, g_stream, kq, vq);
         qr::AttnParams ap{q, o, Hq, M, D, scale, 1, Hkv, kf, vtf, Mp};
         if (e == hipSuccess) e = qr::launch_flash_attn_q8_0(ap, g_stream);
         rc = check(e, "layer attention");

@@ -187,6 +187,7 @@ template <> struct Frag<QUANT_MLX_4BIT_G64> {
 };
 
 constexpr int kSkWaves = 8;
+constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkNT = 4;                  // 16-column tiles per wave
 constexpr int kSkCols = 16 * kSkNT;       // columns per workgroup
 constexpr uint32_t kSkLdsMax = 159 * 1024;  // 160 KB LDS less static allocations
@@ -219,7 +220,7 @@ __host__ __device__ inline SkLayout sk_layout(uint32_t M, uint32_t gpw, uint32_t
 }
 
 template <int F, int MT, int GPW>  // MT: 16-row tiles of M; GPW: 32-groups per wave
-__global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* ws, uint32_t ksplit) {
+__global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmParams p, float* ws, uint32_t ksplit) {
     using FR = Frag<F>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr uint32_t GB = GroupBytes<F>::v;
@@ -243,33 +244,33 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
         auto wr = make_rsrc(p.W + (size_t)n0 * col_bytes, ncols * col_bytes);
         auto xr = make_rsrc(p.X, M * K * 2u);
         constexpr uint32_t WCH = kSkCols * SB / 16;       // 16-byte chunks of the strips
-        constexpr uint32_t WPT = (WCH + 511) / 512;
+        constexpr uint32_t WPT = (WCH + kSkThreads - 1) / kSkThreads;
         constexpr uint32_t xch_row = KC * 2 / 16;
         const uint32_t XCH = M * xch_row;
-        constexpr uint32_t XPT_MAX = (MT * 16 * xch_row + 511) / 512;
+        constexpr uint32_t XPT_MAX = (MT * 16 * xch_row + kSkThreads - 1) / kSkThreads;
         u4_t wv[WPT], xv[XPT_MAX];
 #pragma unroll
         for (uint32_t i = 0; i < WPT; i++) {
-            const uint32_t q = tid + 512 * i;
+            const uint32_t q = tid + kSkThreads * i;
             const uint32_t c = q / (SB / 16), j = q % (SB / 16);
             const uint32_t off = (q < WCH && c < ncols) ? c * col_bytes + ks * SB + 16 * j : kOOB;
             wv[i] = ld_b128(wr, off);
         }
 #pragma unroll
         for (uint32_t i = 0; i < XPT_MAX; i++) {
-            const uint32_t q = tid + 512 * i;
+            const uint32_t q = tid + kSkThreads * i;
             const uint32_t m = q / xch_row, j = q % xch_row;
             const uint32_t off = (q < XCH) ? (m * K + ks * KC) * 2u + 16 * j : kOOB;
             xv[i] = ld_b128(xr, off);
         }
 #pragma unroll
         for (uint32_t i = 0; i < WPT; i++) {
-            const uint32_t q = tid + 512 * i;
+            const uint32_t q = tid + kSkThreads * i;
             if (q < WCH) *reinterpret_cast<u4_t*>(wsb + (q / (SB / 16)) * L.sbp + 16 * (q % (SB / 16))) = wv[i];
         }
 #pragma unroll
         for (uint32_t i = 0; i < XPT_MAX; i++) {
-            const uint32_t q = tid + 512 * i;
+            const uint32_t q = tid + kSkThreads * i;
             if (q < XCH) *reinterpret_cast<u4_t*>(xs + (q / xch_row) * L.xrs + 16 * (q % xch_row)) = xv[i];
         }
     }
@@ -336,14 +337,14 @@ __global__ void __launch_bounds__(512) gemm_skinny_kernel(GemmParams p, float* w
 
     const bool split = ksplit > 1;
     constexpr int NEL = ROWS * kSkCols;
-    constexpr int PER = (NEL + 511) / 512;  // outputs per thread; element idx -> (m = idx / 64, n = idx % 64)
+    constexpr int PER = (NEL + kSkThreads - 1) / kSkThreads;  // outputs per thread; element idx -> (m = idx / 64, n = idx % 64)
     // K split: this split's fp32 partials go to ws [split][M][N] and
     // splitk_reduce_kernel (launched next) sums them in split order;
     // otherwise the sum is the output.
     float* part = split ? ws + (size_t)ks * M * N : nullptr;
 #pragma unroll
     for (int e = 0; e < PER; e++) {
-        const int idx = tid + 512 * e;
+        const int idx = tid + kSkThreads * e;
         const uint32_t m = idx / kSkCols, nl = idx % kSkCols;
         if (idx >= NEL || m >= M || nl >= ncols) continue;
         const int off = (idx / kSkCols) * RS + idx % kSkCols;
@@ -387,7 +388,7 @@ static bool sk_plan(int f, uint32_t M, uint32_t N, uint32_t K, uint32_t* ks_out,
     const uint32_t groups = (N + kSkCols - 1) / kSkCols;
     const uint32_t ng = K / 32;
     for (uint32_t gpw : {4u, 2u, 1u}) {
-        if (ng % (gpw * kSkWaves)) continue;
+        if (ng % (gpw * kSkWaves) || (gpw * kSkWaves * gb) % 16) continue;
         const uint32_t ks = ng / (gpw * kSkWaves);
         if (ks > 16) continue;
         if (groups * ks < 256 && gpw > 1) continue;
@@ -410,6 +411,9 @@ size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K) {
 
 template <int F, int MT, int GPW>
 static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t ks, hipStream_t st) {
+    if constexpr ((GPW * kSkWaves * GroupBytes<F>::v) % 16 != 0) {
+        return hipErrorInvalidValue;  // sk_plan never picks a strip that is not whole 16-byte chunks
+    } else {
     auto kern = gemm_skinny_kernel<F, MT, GPW>;
     const uint32_t groups = (p.N + kSkCols - 1) / kSkCols;
     const size_t lds = sk_layout(p.M, GPW, GroupBytes<F>::v).lds;
@@ -419,10 +423,11 @@ static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t ks, hipStre
         if (e != hipSuccess) return e;
         attr = lds;
     }
-    hipLaunchKernelGGL(kern, dim3(groups, ks), dim3(512), lds, st, p, ws, ks);
+    hipLaunchKernelGGL(kern, dim3(groups, ks), dim3(kSkThreads), lds, st, p, ws, ks);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && ks > 1) e = launch_splitk_reduce(ws, ks, p.M, p.N, false, p.R, p.Y, p.head_D, st);
     return e;
+    }
 }
 
 template <int F, int MT>

@@ -73,8 +73,10 @@ uint32_t kv_padded_len(uint32_t M);
 // K / V ([Hkv, M, D] Q8_0 blocks when from_q8, else fp16) -> the dequantized
 // fp16 cache of the attention kernel (Q8_0 values half(q * half(d)), computed
 // from fp16 inputs by quantizing and dequantizing in registers).
+// From fp16 K / V, the Q8_0 blocks are also written to Kq / Vq when non-null
+// (the layer's Q8_0 KV cache, [Hkv, M, D] blocks of 32 d).
 hipError_t launch_kv_prep(const void* K, const void* V, bool from_q8, _Float16* Kf, _Float16* Vtf, uint32_t Hkv,
-                          uint32_t M, uint32_t D, hipStream_t st);
+                          uint32_t M, uint32_t D, hipStream_t st, uint8_t* Kq = nullptr, uint8_t* Vq = nullptr);
 
 // RMSNorm over rows of X [M, D] (D % 8 == 0): y = fp16(fp16(x r) w), r =
 // 1 / sqrt(mean(x^2) + eps); norm_type 2 uses fp16(1 + w) in place of w.

@@ -82,6 +82,8 @@ SIGNATURES = {
     "m4_bridge_rope": ([_VP, _SZ, _U32, _U32, _U32, _F, _U32, _I], _I),
     "m4_bridge_prefill_layer_ex": ([_VP] * 11 + [_I, _U32, _U32, _U32, _U32, _U32, _U32, _F, _I, _F, _I, _F, _U32,
                                                  _I], _I),
+    "m4_bridge_prefill_layer_ex_kv": ([_VP] * 13 + [_I, _U32, _U32, _U32, _U32, _U32, _U32, _F, _I, _F, _I, _F,
+                                                    _U32, _I], _I),
     "m4_bridge_dequantize": ([_VP, _SZ, _VP, _SZ, _I, _U32, _U32], _I),
     "m4_bridge_set_stream": ([_VP], _I),
     "m4_bridge_get_stream": ([], _VP),

@@ -865,3 +865,41 @@ def test_mlx_g64_projection(bridge, oracle, M, kind):
     tolerance.check_ref(host(Y), oracle.gemm(8, X, W, N), what=f"g64 {kind} M={M}")
     tolerance.check_ref(host(Yr), oracle.gemm(8, X, W, N, R=R), what="g64 residual")
     tolerance.check_ref(host(Yh), oracle.gemm(8, X, W, N, head_D=D), what="g64 direct-head")
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_prefill_layer_writes_its_q8_0_kv_cache(bridge, oracle, rope):
+    """m4_bridge_prefill_layer_ex_kv hands back the layer's Q8_0 KV cache
+    (unified_prefill_engine.mm:548-572): its blocks are the Q8_0 quantization
+    (bit-exact) of the K and V the layer projected -- recomputed here with the
+    head-major projection and RoPE entry points -- and the layer output equals
+    the entry point without the cache outputs, bit for bit."""
+    import torch
+
+    M, dm, Hq, Hkv, D, Nm = 192, 256, 4, 2, 64, 512
+    X = synth.activations(M, dm, 301)
+    shapes = [(Hq * D, dm), (Hkv * D, dm), (Hkv * D, dm), (dm, Hq * D), (Nm, dm), (Nm, dm), (dm, Nm)]
+    Ws = [dev(synth.quantized_weights(0, n, k, 310 + i)) for i, (n, k) in enumerate(shapes)]
+    Xd = dev(X)
+    nb = Hkv * M * D // 32
+    Kq = torch.zeros(nb * 34, dtype=torch.uint8, device="cuda")
+    Vq = torch.zeros(nb * 34, dtype=torch.uint8, device="cuda")
+    out_kv, out = empty16(M, dm), empty16(M, dm)
+    lib = bridge.lib
+    args = (0, M, dm, Hq, Hkv, D, Nm, 0.125, 1, 1e-5, int(rope), 10000.0, 3, 0)
+    ptr = [t.data_ptr() for t in Ws]
+    assert lib.m4_bridge_prefill_layer_ex_kv(Xd.data_ptr(), None, *ptr[:4], None, *ptr[4:], out_kv.data_ptr(),
+                                             Kq.data_ptr(), Vq.data_ptr(), *args) == 0
+    assert lib.m4_bridge_prefill_layer_ex(Xd.data_ptr(), None, *ptr[:4], None, *ptr[4:], out.data_ptr(), *args) == 0
+    assert lib.m4_bridge_prefill_layer_ex_kv(Xd.data_ptr(), None, *ptr[:4], None, *ptr[4:], out.data_ptr(),
+                                             Kq.data_ptr(), None, *args) == -2
+    K = empty16(Hkv, M, D)
+    V = empty16(Hkv, M, D)
+    bridge.dispatch_head_gemm(Xd, Ws[1], K, 0, M, Hkv, D, dm)
+    bridge.dispatch_head_gemm(Xd, Ws[2], V, 0, M, Hkv, D, dm)
+    if rope:
+        bridge.rope(K, theta=10000.0, offset=3)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(out_kv).view(np.uint16), host(out).view(np.uint16))
+    np.testing.assert_array_equal(host(Kq), oracle.quantize_q8_0(host(K)))
+    np.testing.assert_array_equal(host(Vq), oracle.quantize_q8_0(host(V)))
