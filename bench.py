@@ -18,7 +18,10 @@ M=33/128/2048, K=4096.  One JSON line on stdout.
 A step is one projection (or one layer) over one batch.  W untimed warmup
 steps run eagerly; the K timed steps are captured once into a HIP graph and
 replayed, so the timed region holds back-to-back kernels with no host launch
-gaps.  Weights rotate over enough device copies (> 512 MB) that every step
+gaps.  Each timed region is one replay of exactly K steps between two events
+on the stream the kernels run on; it is repeated --repeats times (default 5)
+and the median per-step time is reported (single replays vary by a few
+percent).  Weights rotate over enough device copies (> 512 MB) that every step
 reads them from HBM, not from the 256 MB Infinity Cache.  All inputs are
 resident in HBM before timing starts.
 """
@@ -50,6 +53,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="all", help="comma list of config names or 'all'")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--repeats", type=int, default=5, help="timed replays of the K steps (median reported)")
     ap.add_argument("--no-probes", action="store_true", help="skip the on-device HBM / MFMA ceiling probes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -59,8 +63,8 @@ class Timer:
     """Times `steps` calls of fn(i) on the current stream: eager warmup, then a
     HIP-graph capture of the timed steps replayed between two events."""
 
-    def __init__(self, bridge, warmup: int, steps: int):
-        self.b, self.warmup, self.steps = bridge, warmup, steps
+    def __init__(self, bridge, warmup: int, steps: int, repeats: int = 5):
+        self.b, self.warmup, self.steps, self.repeats = bridge, warmup, steps, repeats
 
     def run(self, fn) -> float:
         import torch
@@ -85,18 +89,24 @@ class Timer:
             mode = "eager"
             self.b.lib.m4_bridge_set_stream(s.cuda_stream)
             torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(s)
-        if mode == "graph":
-            g.replay()
-        else:
-            for i in range(self.steps):
-                fn(i)
-        e1.record(s)
-        torch.cuda.synchronize()
+        # REPEATS timed replays of the K steps; the median is reported (one
+        # replay alone varies by a few percent from run to run)
+        times = []
+        for _ in range(self.repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(s)
+            if mode == "graph":
+                g.replay()
+            else:
+                for i in range(self.steps):
+                    fn(i)
+            e1.record(s)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / self.steps)
         self.mode = mode
-        return e0.elapsed_time(e1) / self.steps  # ms per step
+        self.spread = (min(times), max(times))
+        return sorted(times)[len(times) // 2]  # ms per step
 
 
 def rotated(t, nbytes_each: int):
@@ -422,7 +432,7 @@ def main():
 
     b = m4_bridge.HIPBridge.get_instance(os.environ.get("M4_BRIDGE_LIB_PATH") or PKG / "libm4_bridge.so")
     assert b.init(), b.last_error()
-    timer = Timer(b, a.warmup, a.steps)
+    timer = Timer(b, a.warmup, a.steps, a.repeats)
     want = None if a.configs == "all" else set(a.configs.split(","))
 
     def on(name):
