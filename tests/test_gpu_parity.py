@@ -903,3 +903,25 @@ def test_prefill_layer_writes_its_q8_0_kv_cache(bridge, oracle, rope):
     np.testing.assert_array_equal(host(out_kv).view(np.uint16), host(out).view(np.uint16))
     np.testing.assert_array_equal(host(Kq), oracle.quantize_q8_0(host(K)))
     np.testing.assert_array_equal(host(Vq), oracle.quantize_q8_0(host(V)))
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3, 8])
+@pytest.mark.parametrize("M", [1, 16, 33, 64])
+def test_small_m_wide_n(bridge, oracle, fmt, M):
+    """Small M, wide ragged N (last 64-column group partly out of range), K
+    split across workgroups: standard, residual and direct-head outputs."""
+    K, N = 2048, 4096 + 48
+    X = synth.activations(M, K, 600 + M)
+    W = synth.quantized_weights(fmt, N, K, 601 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    R = synth.activations(M, N, 602)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    H, D = N // 16, 16
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    bridge.synchronize()
+    assert maxdiff(host(Y), oracle.gemm(fmt, X, W, N)) <= TOL
+    assert maxdiff(host(Yr), oracle.gemm(fmt, X, W, N, R=R)) <= TOL
+    assert maxdiff(host(Yh), oracle.gemm(fmt, X, W, N, head_D=D)) <= TOL
