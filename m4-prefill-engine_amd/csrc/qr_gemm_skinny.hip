@@ -462,15 +462,6 @@ bool skinny_supported(const GemmParams& p) {
 
 hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, hipStream_t st) {
     switch (p.format) {
-            case QUANT_Q4_0: return launch_st_m<QUANT_Q4_0>(p, ct, st);
-            case QUANT_MLX_4BIT: return launch_st_m<QUANT_MLX_4BIT>(p, ct, st);
-            case QUANT_Q4_K: return launch_st_m<QUANT_Q4_K>(p, ct, st);
-            case QUANT_TERNARY_1_58: return launch_st_m<QUANT_TERNARY_1_58>(p, ct, st);
-            case QUANT_MLX_4BIT_G64: return launch_st_m<QUANT_MLX_4BIT_G64>(p, ct, st);
-            default: return hipErrorInvalidValue;
-        }
-    }
-    switch (p.format) {
         case QUANT_Q4_0: return launch_sk_m<QUANT_Q4_0>(p, ws, st);
         case QUANT_MLX_4BIT: return launch_sk_m<QUANT_MLX_4BIT>(p, ws, st);
         case QUANT_Q4_K: return launch_sk_m<QUANT_Q4_K>(p, ws, st);
