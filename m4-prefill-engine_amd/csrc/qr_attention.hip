@@ -17,6 +17,8 @@
 //    the matching key order in the V^T A-operand reads (two ds_read_b64).
 //  * fp32 running max / sum / output accumulators (the reference keeps
 //    S, P and O in half); the output is rounded to fp16 once.
+#include <type_traits>
+
 #include "qr_device.h"
 #include "qr_kernels.h"
 
@@ -252,7 +254,7 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kBKV * KROW];
     __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VROW];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, j = lane & 31;
     const int M = (int)p.M;
     const int qtiles = (M + kBQ - 1) / kBQ;
@@ -478,7 +480,7 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     auto Ks = [&](int buf) { return smem + buf * KT; };
     auto Vt = [&](int buf) { return smem + 2 * KT + buf * VT; };
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave >> 2, wq = wave & 3;
     const int g = lane >> 5, j = lane & 31;
     const int M = (int)p.M, Mp = (int)p.Mp;
@@ -566,7 +568,10 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     };
 
     // one key tile (or its 32-key half ks0) for the wave's current queries
-    auto compute = [&](int kt, int ks0, int nks) {
+    // nks (32-key halves of the tile handled) is a compile-time constant in
+    // each call, so every loop below unrolls without runtime exits
+    auto compute = [&](int kt, int ks0, auto nks_c) {
+        constexpr int nks = decltype(nks_c)::value;
         const int k0 = kt * kBKV;
         if (k0 + 32 * ks0 > qw + 31) return;  // the keys handled lie above this wave's diagonal
         const int my_q = qw + j;
@@ -664,9 +669,9 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     };
     auto step = [&](int t) {
         if (t < Tl) {
-            compute(t, 0, 2);          // group 0: light queries, group 1: heavy queries
+            compute(t, 0, std::integral_constant<int, 2>{});   // group 0: light queries, group 1: heavy queries
         } else {
-            compute(t, grp, 1);        // both: heavy queries, one 32-key half each
+            compute(t, grp, std::integral_constant<int, 1>{});  // both: heavy queries, one 32-key half each
         }
     };
 

@@ -114,7 +114,7 @@ gemm_rb_kernel(GemmParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int wrow = wave / C::WC, wcolg = wave % C::WC;  // this wave's row group and column group
     const int h = lane >> 5;     // quant group of the step this lane owns
     const int c32 = lane & 31;
