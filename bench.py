@@ -344,7 +344,7 @@ def bench_copy(timer, nbytes: int):
             "gbs": round(2.0 * nbytes / (ms * 1e-3) / 1e9, 1), "timing": timer.mode}
 
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_rb_mlx_m128_traffic.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "hbm_traffic_router_kernels.md"
 # Sources of the headline kernel: a traffic figure measured on other
 # versions of these files is stale and is not reported.
 KERNEL_SOURCES = ("qr_gemm.hip", "qr_gemm_host.hip", "qr_gemm_shapes.h", "qr_decode.h", "qr_device.h",
@@ -496,7 +496,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": traffic,
                      "traffic_note": traffic_note,
-                     "kernel": "gemm_rb_kernel<MLX_4BIT, 4, 1, 4> (128x128 tiles, K split 2)", "hbm_frac": head.get("frac_hbm")},
+                     "kernel": "gemm_rb_kernel<MLX_4BIT, 4, 1, 4> (128x128 tiles, K split 2) + splitk_reduce_kernel", "hbm_frac": head.get("frac_hbm")},
         "per_config": per,
     }
     if not a.no_probes:
