@@ -452,33 +452,38 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 }
 
 // --------------------------------------------------------------------------
-// Balanced causal attention over the fp16 cache (D = 64): one workgroup of 8
-// waves per (light, heavy) query-tile pair of one head -- query tiles a and
-// qtiles - 1 - a -- so every workgroup carries the same number of key tiles
-// and every SIMD keeps two waves busy until the end (with one query tile per
-// workgroup, a CU's light workgroup finishes early and its SIMDs are left
-// with a single wave for most of the kernel).  Wave group 0 takes the light
-// tile's queries over key tiles [0, Tl), group 1 the heavy tile's over [0, Tl);
-// on key tiles [Tl, Th) both groups take the heavy queries, group 0 the first
-// 32 keys of each tile and group 1 the last 32; at the end group 0's partial
-// softmax state for the heavy queries is merged into group 1's through LDS.
-// The per-tile arithmetic is that of flash_attn_q8_0_kernel.
+// Software-pipelined causal attention over the fp16 cache (D = 64), with the
+// query-tile pairing that balances the causal work: one workgroup of 8 waves per
+// (light, heavy) pair of 128-query tiles -- a and qtiles - 1 - a -- so every
+// workgroup carries the same work.  Key tiles are 128 keys (one barrier per
+// 128 keys); a tile is four 32-key units.  Group 0 takes the light tile's
+// queries and group 1 the heavy tile's on the key tiles both need; on the
+// heavy tile's remaining key tiles group 0 takes units 0-1 and group 1 units
+// 2-3 of each tile for the heavy queries, and group 0's partial softmax state
+// is merged into group 1's at the end.  Units whose keys all lie above a
+// wave's diagonal are skipped.
+//
+// Pipelining: while the softmax of unit u runs on the VALU, the S^T = K . Q^T
+// MFMAs of unit u + 1 and the O^T += V^T . P^T MFMAs of unit u are issued from
+// the same fenced instruction sequence, so the matrix pipe and the vector ALU
+// work side by side inside every wave.  K/V tiles sit in a 3-deep LDS ring
+// (tile t read, tile t + 1 read by the look-ahead S, tile t + 2 being
+// written).  Arithmetic per unit: log2-unit softmax with the scale folded into
+// one fma, a lazily moved reference point (threshold 2^8, decided per lane
+// half, the halves combined only when it moves), fp32 state, P rounded to
+// fp16 for the MFMA and for the row sums.
 // --------------------------------------------------------------------------
-#ifndef QR_ATTN_PREF
-#define QR_ATTN_PREF 2
-#endif
+constexpr int kPKV = 128;  // keys per tile of the pipelined kernel
+
 template <int D>
-__global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
-    constexpr int KROW = D + 8, VROW = kBKV + 8, DT = D / 32;
+__global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
+    static_assert(D == 64, "chunk schedule and per-thread staging written for D = 64");
+    constexpr int KROW = D + 8, VROW = kPKV + 8, DT = D / 32;
     constexpr int NT = 512;
-    constexpr int KCH = kBKV * (D / 8) / NT;   // 16-byte K chunks per thread and tile
-    constexpr int VCH = D * (kBKV / 8) / NT;   // 16-byte V^T chunks per thread and tile
-    static_assert(KCH >= 1 && VCH >= 1, "whole chunks per thread");
-    // one LDS array: K tiles [2][key][d], V^T tiles [2][d][key]; reused by the final merge
-    constexpr int KT = kBKV * KROW, VT = D * VROW;
-    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * KT + 2 * VT];
-    auto Ks = [&](int buf) { return smem + buf * KT; };
-    auto Vt = [&](int buf) { return smem + 2 * KT + buf * VT; };
+    constexpr int KT = kPKV * KROW, VT = D * VROW, TILE = KT + VT;
+    constexpr int NBUF = 3;
+    constexpr int KCH = kPKV * (D / 8) / NT, VCH = D * (kPKV / 8) / NT;  // 16-byte chunks per thread
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave >> 2, wq = wave & 3;
@@ -486,8 +491,8 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     const int M = (int)p.M, Mp = (int)p.Mp;
     const int qtiles = (M + kBQ - 1) / kBQ;
     const int pr = (int)blockIdx.x / (int)p.H, h = (int)blockIdx.x % (int)p.H;
-    const int qa = pr, qb = qtiles - 1 - pr;   // light and heavy query tiles (qa <= qb)
-    auto tiles_for = [&](int qt) { return (min((qt + 1) * kBQ, M) - 1) / kBKV + 1; };
+    const int qa = pr, qb = qtiles - 1 - pr;
+    auto tiles_for = [&](int qt) { return (min((qt + 1) * kBQ, M) - 1) / kPKV + 1; };
     const int Tl = qa == qb ? 0 : tiles_for(qa);
     const int Th = tiles_for(qb);
 
@@ -498,9 +503,12 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
     auto vr = make_rsrc(p.Vtf + (size_t)hk * Mp * D, cbytes);
     auto qr_ = make_rsrc(p.Q + (size_t)h * head_elems, (uint32_t)(head_elems * 2));
 
-    struct Raw { u4_t k[KCH]; u4_t v[VCH]; };
+    // ---- K / V^T tiles: fetched 3 tiles ahead into registers, written to
+    // the LDS ring 2 tiles ahead.  Keys past Mp read zeros (K) or finite
+    // cache values of the next row (V^T), both masked out. ----
+    struct Raw { u4_t k[KCH], v[VCH]; };
     auto fetch = [&](int t, Raw& r) {
-        const int k0 = t * kBKV;
+        const int k0 = t * kPKV;
 #pragma unroll
         for (int i = 0; i < KCH; i++) {
             const int c = tid + NT * i;
@@ -509,47 +517,63 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
             const int c = tid + NT * i;
-            r.v[i] = ld_b128(vr, (uint32_t)((c / 8) * Mp + k0 + (c % 8) * 8) * 2u);
+            r.v[i] = ld_b128(vr, (uint32_t)((c / (kPKV / 8)) * Mp + k0 + (c % (kPKV / 8)) * 8) * 2u);
         }
     };
-    auto stage = [&](const Raw& r, int buf) {
+    auto kbuf = [&](int slot) { return smem + slot * TILE; };
+    auto vbuf = [&](int slot) { return smem + slot * TILE + KT; };
+    auto stage = [&](const Raw& r, int slot) {
 #pragma unroll
         for (int i = 0; i < KCH; i++) {
             const int c = tid + NT * i;
-            *reinterpret_cast<u4_t*>(Ks(buf) + (c / (D / 8)) * KROW + (c % (D / 8)) * 8) = r.k[i];
+            *reinterpret_cast<u4_t*>(kbuf(slot) + (c / (D / 8)) * KROW + (c % (D / 8)) * 8) = r.k[i];
         }
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
             const int c = tid + NT * i;
-            *reinterpret_cast<u4_t*>(Vt(buf) + (c / 8) * VROW + (c % 8) * 8) = r.v[i];
+            *reinterpret_cast<u4_t*>(vbuf(slot) + (c / (kPKV / 8)) * VROW + (c % (kPKV / 8)) * 8) = r.v[i];
         }
     };
 
-    // scale in log2 units; a negative scale flips the sign of Q (exact)
-    float c = p.scale * 1.4426950408889634f;
+    // ---- this wave's units (key start 32 * unit index within the keys):
+    // segment 1 = units 0..3 of tiles [0, Tl) (light queries for group 0,
+    // heavy for group 1), segment 2 = units 2 grp, 2 grp + 1 of tiles
+    // [Tl, Th) (heavy queries); each segment keeps the prefix whose first key
+    // is at or below the wave's last query ----
+    const int qwL = qa * kBQ + wq * 32, qwH = qb * kBQ + wq * 32;
+    const int n1 = grp == 0 ? (Tl > 0 ? min(4 * Tl, (qwL + 31) / 32 + 1) : 0) : 4 * Tl;
+    int n2 = 0;
+    for (int t = Tl; t < Th; t++)
+        for (int e = 0; e < 2; e++)
+            n2 += (t * kPKV + (2 * grp + e) * 32 <= qwH + 31) ? 1 : 0;
+    const int ntot = n1 + n2;
+
+    float c = p.scale * 1.4426950408889634f;  // log2 units
     const bool neg = c < 0.0f;
     if (neg) c = -c;
 
-    // per-wave state: the queries qw .. qw + 31 it currently owns
-    int qw = 0;
     h8_t qf[D / 16];
-    float m_run = -INFINITY;
-    f16v_t o[DT + 1];
-    const _Float16 one = j == 0 ? (_Float16)1.0f : (_Float16)0.0f;
-    const h8_t ones = {one, one, one, one, one, one, one, one};
-    auto begin = [&](int qt) {  // take the queries of tile qt, fresh state
-        qw = qt * kBQ + wq * 32;
-        const int my_q = qw + j;
+    auto load_q = [&](int qw, h8_t* dst) {
 #pragma unroll
         for (int kk = 0; kk < D / 16; kk++) {
+            const int my_q = qw + j;
             const uint32_t off = my_q < M ? ((uint32_t)my_q * D + kk * 16 + 8 * g) * 2u : kOOB;
-            qf[kk] = __builtin_bit_cast(h8_t, ld_b128(qr_, off));
-            if (neg) qf[kk] = -qf[kk];
+            dst[kk] = __builtin_bit_cast(h8_t, ld_b128(qr_, off));
+            if (neg) dst[kk] = -dst[kk];
         }
-        m_run = -INFINITY;
-#pragma unroll
-        for (int t = 0; t <= DT; t++) o[t] = f16v_t{};
     };
+    // group 0 starts on the light queries when it has any, else on the heavy ones
+    bool light = grp == 0 && n1 > 0;
+    int qw = light ? qwL : qwH;
+    load_q(qw, qf);
+
+    float m_run = -INFINITY;
+    float l_run = 0.0f;  // this lane's half of the row sum of P
+    f16v_t o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++) o[t] = f16v_t{};
+    const h2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+
     auto store = [&](float inv) {
         const int my_q = qw + j;
         if (my_q >= M) return;
@@ -567,151 +591,212 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
             }
     };
 
-    // one key tile (or its 32-key half ks0) for the wave's current queries
-    // nks (32-key halves of the tile handled) is a compile-time constant in
-    // each call, so every loop below unrolls without runtime exits
-    auto compute = [&](int kt, int ks0, auto nks_c) {
-        constexpr int nks = decltype(nks_c)::value;
-        const int k0 = kt * kBKV;
-        if (k0 + 32 * ks0 > qw + 31) return;  // the keys handled lie above this wave's diagonal
-        const int my_q = qw + j;
-        const _Float16* Kb = Ks(kt & 1);
-        const _Float16* Vb = Vt(kt & 1);
-        h8_t ka[2][D / 16];
-        f16v_t s[2];
+    // ---- one unit: S^T of unit (slot, hh) is in s_in; the look-ahead unit's
+    // S^T (ring slot nsl, unit hn) is computed into s_out beside the softmax;
+    // MASK applies the causal / length mask to s_in first ----
+    const int kbase = j * KROW + 8 * g, vbase = j * VROW + 4 * g;
+    auto unit_core = [&](int slot, int hh, int key0, bool mask, f16v_t& s_in, int nsl, int hn, f16v_t& s_out) {
+        if (mask) {
+            const int my_q = qw + j;
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e >= nks) break;
-#pragma unroll
-            for (int kk = 0; kk < D / 16; kk++)
-                ka[e][kk] = *reinterpret_cast<const h8_t*>(Kb + ((ks0 + e) * 32 + j) * KROW + kk * 16 + 8 * g);
+            for (int r = 0; r < 16; r++) {
+                const int key = key0 + 8 * (r >> 2) + 4 * g + (r & 3);
+                s_in[r] = (key <= my_q && key < M) ? s_in[r] : -INFINITY;
+            }
         }
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e >= nks) break;
-            s[e] = f16v_t{};
-#pragma unroll
-            for (int kk = 0; kk < D / 16; kk++)
-                s[e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[e][kk], qf[kk], s[e], 0, 0, 0);
-        }
-        u4_t va[2][2][DT];
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e >= nks) break;
+        // V^T fragments of this unit, K fragments of the look-ahead unit
+        u4_t va[2][DT];
+        {
+            const _Float16* Vb = smem + slot * TILE + KT + hh * 32 + vbase;
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-                for (int t = 0; t < DT; t++) {
-                    const _Float16* row = Vb + (t * 32 + j) * VROW + (ks0 + e) * 32 + t2 * 16 + 4 * g;
+                for (int tt = 0; tt < DT; tt++) {
+                    const _Float16* row = Vb + tt * 32 * VROW + t2 * 16;
                     const u2_t lo = *reinterpret_cast<const u2_t*>(row);
                     const u2_t hi = *reinterpret_cast<const u2_t*>(row + 8);
-                    va[e][t2][t] = u4_t{lo.x, lo.y, hi.x, hi.y};
+                    va[t2][tt] = u4_t{lo.x, lo.y, hi.x, hi.y};
                 }
         }
-        if (k0 + 32 * (ks0 + nks) - 1 > qw) {  // keys crossing the diagonal: causal mask
+        h8_t kn_[D / 16];
+        {
+            const _Float16* Kb = smem + nsl * TILE + hn * 32 * KROW + kbase;
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                if (e >= nks) break;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = k0 + (ks0 + e) * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    s[e][r] = (key <= my_q && key < M) ? s[e][r] : -INFINITY;
-                }
-            }
+            for (int kk = 0; kk < D / 16; kk++)
+                kn_[kk] = *reinterpret_cast<const h8_t*>(Kb + kk * 16);
         }
-        float tmax = -INFINITY;
+        // Row maximum: each lane's half (16 keys) decides whether the shared
+        // reference point must move; only then are the two halves combined.
+        float mx[4];  // a shallow tree of three-input maxima
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e >= nks) break;
-#pragma unroll
-            for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s[e][r]);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_cand = tmax * c;
-        float alpha = 1.0f;
-        if (__any(m_cand > m_run + 8.0f)) {  // lazy reference point (P <= 2^8 otherwise)
-            const float m_new = fmaxf(m_run, m_cand);
-            alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        for (int q = 0; q < 4; q++) mx[q] = fmaxf(fmaxf(s_in[4 * q], s_in[4 * q + 1]), fmaxf(s_in[4 * q + 2], s_in[4 * q + 3]));
+        const float hmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+        const float m_cand = hmax * c;
+        if (__any(m_cand > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, fmaxf(m_cand, __shfl_xor(m_cand, 32)));
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
+#pragma unroll
+            for (int tt = 0; tt < DT; tt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[tt][r] *= alpha;
+            l_run *= alpha;
         }
-        uint32_t pk[2][8];
+        // --- fenced chunks: look-ahead S MFMAs and this unit's O MFMAs
+        // interleaved with this unit's exponentials ---
+        uint32_t pk[8];
+        float e[16];
+        auto exps = [&](int r0) {  // exp2 of accumulator rows r0 .. r0 + 3
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e >= nks) break;
+            for (int r = r0; r < r0 + 4; r++)
+                e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_in[r], c, -m_run));
+        };
+        auto cvts = [&](int r0) {  // P (fp16 pairs) of rows r0 .. r0 + 3
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const f2_t ee = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[e][r], c, -m_run)),
-                                 __builtin_amdgcn_exp2f(__builtin_fmaf(s[e][r + 1], c, -m_run))};
-                pk[e][r >> 1] = as_u32(__builtin_convertvector(ee, h2_t));
+            for (int r = r0; r < r0 + 4; r += 2) {
+                const h2_t pp = __builtin_convertvector((f2_t){e[r], e[r + 1]}, h2_t);
+                pk[r >> 1] = as_u32(pp);
+                l_run = __builtin_amdgcn_fdot2(pp, one2, l_run, false);  // row sum of the rounded P
             }
-        }
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int t = 0; t < DT; t++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[t][r] *= alpha;
-            o[DT][0] *= alpha;
-        }
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e >= nks) break;
-#pragma unroll
-            for (int t2 = 0; t2 < 2; t2++) {
-                const h8_t b = __builtin_bit_cast(
-                    h8_t, u4_t{pk[e][4 * t2], pk[e][4 * t2 + 1], pk[e][4 * t2 + 2], pk[e][4 * t2 + 3]});
-#pragma unroll
-                for (int t = 0; t < DT; t++)
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[e][t2][t]), b, o[t], 0,
-                                                                  0, 0);
-                o[DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, b, o[DT], 0, 0, 0);
-            }
-        }
+        };
+        auto pv = [&](int t2, int tt) {
+            const h8_t b = __builtin_bit_cast(h8_t, u4_t{pk[4 * t2], pk[4 * t2 + 1], pk[4 * t2 + 2], pk[4 * t2 + 3]});
+            o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[t2][tt]), b, o[tt], 0, 0, 0);
+        };
+        static_assert(DT == 2, "chunk schedule written for D = 64");
+        // each exponential is converted one chunk after it is issued, and each
+        // O MFMA follows the conversions it needs by a chunk where possible
+        __builtin_amdgcn_sched_barrier(0);
+        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[0], qf[0], f16v_t{}, 0, 0, 0);
+        exps(0);
+        __builtin_amdgcn_sched_barrier(0);
+        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[1], qf[1], s_out, 0, 0, 0);
+        exps(4);
+        cvts(0);
+        __builtin_amdgcn_sched_barrier(0);
+        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[2], qf[2], s_out, 0, 0, 0);
+        exps(8);
+        cvts(4);
+        __builtin_amdgcn_sched_barrier(0);
+        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[3], qf[3], s_out, 0, 0, 0);
+        pv(0, 0);
+        exps(12);
+        cvts(8);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(0, 1);
+        cvts(12);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(1, 0);
+        pv(1, 1);
+        __builtin_amdgcn_sched_barrier(0);
     };
-    auto step = [&](int t) {
-        if (t < Tl) {
-            compute(t, 0, std::integral_constant<int, 2>{});   // group 0: light queries, group 1: heavy queries
-        } else {
-            compute(t, grp, std::integral_constant<int, 1>{});  // both: heavy queries, one 32-key half each
-        }
+    auto scores_now = [&](int slot, int hh, f16v_t& s) {
+        const _Float16* Kb = smem + slot * TILE + hh * 32 * KROW + kbase;
+        h8_t ka[D / 16];
+#pragma unroll
+        for (int kk = 0; kk < D / 16; kk++) ka[kk] = *reinterpret_cast<const h8_t*>(Kb + kk * 16);
+        s = f16v_t{};
+#pragma unroll
+        for (int kk = 0; kk < D / 16; kk++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kk], qf[kk], s, 0, 0, 0);
+    };
+    auto switch_to_heavy = [&]() {  // light queries done: write them, take the heavy ones
+        store(1.0f / (l_run + __shfl_xor(l_run, 32)));
+        light = false;
+        qw = qwH;
+        load_q(qwH, qf);
+        m_run = -INFINITY;
+        l_run = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < DT; tt++) o[tt] = f16v_t{};
     };
 
-    begin(grp == 0 && Tl > 0 ? qa : qb);
-    // raw K / V^T tiles fetched R tiles ahead (a ring of R register sets,
-    // loop unrolled by R so every slot index is static)
-    constexpr int R = QR_ATTN_PREF;
-    Raw raw[R];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-        if (r < Th) fetch(r, raw[r]);
-    stage(raw[0], 0);
+    // ---- prologue ----
+    Raw raw;
+    fetch(0, raw);
+    stage(raw, 0);
+    fetch(1, raw);
+    stage(raw, 1);
+    fetch(2, raw);
     __syncthreads();
-    for (int t0 = 0; t0 < Th; t0 += R) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int t = t0 + r;
-            if (t >= Th) break;
-            if (t + R < Th) fetch(t + R, raw[r]);
-            step(t);
-            if (grp == 0 && t + 1 == Tl) {  // light tile done: write it, take the heavy queries
-                store(1.0f / __shfl(o[DT][0], j, 64));
-                begin(qb);
+
+    int k = 0;          // next unit of this wave
+    bool have = false;  // sA holds S^T of unit k
+    f16v_t sA, sB;
+    // units of this wave in tile t, and the first of them
+    auto count_in = [&](int t) {
+        return t < Tl ? min(max(n1 - 4 * t, 0), 4) : min(max(n2 - 2 * (t - Tl), 0), 2);
+    };
+    auto first_h = [&](int t) { return t < Tl ? 0 : 2 * grp; };
+
+    int slot = 0;  // ring slot of tile t
+    for (int t = 0; t < Th; t++) {
+        {
+            const int nslot = slot == NBUF - 1 ? 0 : slot + 1;
+            const int sslot = nslot == NBUF - 1 ? 0 : nslot + 1;  // tile t + 2
+            if (t + 2 < Th) {  // raw holds tile t + 2 (fetched one tile ago)
+                stage(raw, sslot);
+                fetch(t + 3, raw);
             }
-            if (t + 1 < Th) stage(raw[(r + 1) % R], (t + 1) & 1);
+            const int cnt = count_in(t);
+            const int h0 = first_h(t);
+            const int key_t = t * kPKV;
+            // look-ahead of the tile's last unit: the first unit of tile t + 1,
+            // when this wave has one and it uses the same queries
+            const bool set_ends = light && k + cnt == n1;
+            const bool next_ok = !set_ends && t + 1 < Th && count_in(t + 1) > 0;
+            const int h_next = next_ok ? first_h(t + 1) : h0;
+            const int s_next = next_ok ? nslot : slot;
+            const bool full = cnt == (t < Tl ? 4 : 2);
+            const bool unmasked = key_t + kPKV - 1 <= qw && key_t + kPKV <= M;
+            if (full && unmasked) {
+                // fast path: straight-line units, scores ping-ponging between sA and sB
+                if (!have) scores_now(slot, h0, sA);
+                unit_core(slot, h0, 0, false, sA, slot, h0 + 1, sB);
+                if (cnt == 4) {
+                    unit_core(slot, h0 + 1, 0, false, sB, slot, h0 + 2, sA);
+                    unit_core(slot, h0 + 2, 0, false, sA, slot, h0 + 3, sB);
+                    unit_core(slot, h0 + 3, 0, false, sB, s_next, h_next, sA);
+                } else {
+                    unit_core(slot, h0 + 1, 0, false, sB, s_next, h_next, sA);
+                }
+                k += cnt;
+                have = next_ok;
+                if (set_ends) switch_to_heavy();
+            } else {
+                // general path: up to four units, each with the mask where needed
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (u < cnt) {
+                        const int hh = h0 + u;
+                        if (!have) scores_now(slot, hh, sA);
+                        const bool last = u + 1 == cnt;
+                        const int nsl = last ? s_next : slot;
+                        const int hn = last ? h_next : hh + 1;
+                        const int key0 = key_t + hh * 32;
+                        unit_core(slot, hh, key0, key0 + 31 > qw || key0 + 31 >= M, sA, nsl, hn, sB);
+                        sA = sB;
+                        have = !last || next_ok;
+                    }
+                }
+                k += cnt;
+                if (set_ends) switch_to_heavy();
+            }
             __syncthreads();
+            slot = nslot;
         }
     }
 
     // ---- merge group 0's partial state for the heavy queries into group 1's ----
-    constexpr int SW = DT * 16 + 2;  // floats per lane: o[0..DT-1], row 0 of o[DT], m
+    constexpr int SW = DT * 16 + 2;
     float* X = reinterpret_cast<float*>(smem);
-    static_assert(4 * 64 * SW * 4 <= (int)sizeof(smem), "merge buffer fits the tile stages");
+    static_assert(4 * 64 * SW * 4 <= NBUF * TILE * 2, "merge buffer fits the tile ring");
     if (grp == 0) {
         float* x = X + (wq * 64 + lane);
 #pragma unroll
         for (int t = 0; t < DT; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) x[(t * 16 + r) * 256] = o[t][r];
-        x[(DT * 16) * 256] = o[DT][0];
+        x[(DT * 16) * 256] = l_run;
         x[(DT * 16 + 1) * 256] = m_run;
     }
     __syncthreads();
@@ -725,26 +810,30 @@ __global__ void __launch_bounds__(512) flash_attn_pair_kernel(AttnParams p) {
         for (int t = 0; t < DT; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) o[t][r] = o[t][r] * fb + x[(t * 16 + r) * 256] * fa;
-        o[DT][0] = o[DT][0] * fb + x[(DT * 16) * 256] * fa;
-        const float l = __shfl(o[DT][0], j, 64);
+        const float lh = l_run * fb + x[(DT * 16) * 256] * fa;
+        const float l = lh + __shfl_xor(lh, 32);
         store(l > 0.0f ? 1.0f / l : 0.0f);
     }
 }
+constexpr size_t kPipeLds = 3 * (size_t)(kPKV * (64 + 8) + 64 * (kPKV + 8)) * 2;
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
     // the kernels read the dequantized fp16 cache (launch_kv_prep)
     if (p.Kf == nullptr || p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV) return hipErrorInvalidValue;
-#ifndef QR_ATTN_PAIR
-#define QR_ATTN_PAIR 1
-#endif
-    if (QR_ATTN_PAIR && p.D == 64) {
+    if (p.D == 64) {
         const uint32_t qtiles = (p.M + kBQ - 1) / kBQ;
-        hipLaunchKernelGGL((flash_attn_pair_kernel<64>), dim3(((qtiles + 1) / 2) * p.H), dim3(512), 0, st, p);
+        static bool attr = false;  // the 3-tile ring needs more than the default 64 KB of LDS
+        if (!attr) {
+            const hipError_t e = hipFuncSetAttribute((const void*)flash_attn_pipe_kernel<64>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPipeLds);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        hipLaunchKernelGGL((flash_attn_pipe_kernel<64>), dim3(((qtiles + 1) / 2) * p.H), dim3(512), kPipeLds, st, p);
         return hipGetLastError();
     }
     switch (p.D) {
-        case 64: hipLaunchKernelGGL((flash_attn_q8_0_kernel<64>), grid, dim3(256), 0, st, p); break;
         case 128: hipLaunchKernelGGL((flash_attn_q8_0_kernel<128>), grid, dim3(256), 0, st, p); break;
         default: return hipErrorInvalidValue;
     }
