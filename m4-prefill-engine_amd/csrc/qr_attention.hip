@@ -664,6 +664,9 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
             o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[t2][tt]), b, o[tt], 0, 0, 0);
         };
         static_assert(DT == 2, "chunk schedule written for D = 64");
+        // raised wave priority for the interleaved block: the SIMD's other
+        // wave (in its row-max / fragment-read phase) yields issue slots to it
+        __builtin_amdgcn_s_setprio(1);
         // each exponential is converted one chunk after it is issued, and each
         // O MFMA follows the conversions it needs by a chunk where possible
         __builtin_amdgcn_sched_barrier(0);
@@ -689,6 +692,7 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
         pv(1, 0);
         pv(1, 1);
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
     };
     auto scores_now = [&](int slot, int hh, f16v_t& s) {
         const _Float16* Kb = smem + slot * TILE + hh * 32 * KROW + kbase;

@@ -8,9 +8,9 @@ namespace qr {
 
 // Shapes {TM, TN, NW, WR}: NW waves in WR row groups; BM = 32 TM WR,
 // BN = 32 TN NW / WR.
-//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K: QR_RB_BIG_K,
-//                  default 4, 1, 8 -> 128 x 256 with two waves per SIMD, whose
-//                  heavier decode then overlaps the other wave's MFMAs)
+//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K and ternary:
+//                  QR_RB_BIG_K, default 4, 1, 8 -> 128 x 256 with two waves per
+//                  SIMD, whose heavier decode then overlaps the other wave's MFMAs)
 //   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
 //                  of 128 x 256 at the same K split, half the reduction)
 //   4 (M <  1024, last 128-row tile at most half full, cheap-decode formats):
@@ -51,7 +51,10 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     // one tile shape: fewer instances of their heavy fp64 decode to compile.
     if (format == QUANT_VAR_RATE_AFFINE || format == QUANT_EXL3) return 1;
     if (M >= 1024) {
-        if (format == QUANT_Q4_K) return 3;
+        // the heavier decodes (Q4_K's fp32 affine, ternary's 2-bit fields) run
+        // best as two waves per SIMD, one decoding while the other multiplies
+        // (ternary M = 2048: 68-70 us vs 76 us with one wave per SIMD)
+        if (format == QUANT_Q4_K || format == QUANT_TERNARY_1_58) return 3;
         const uint32_t big_tiles = ((M + 127) / 128) * ((N + 255) / 256);
         if (QR_RB_MID_FILL && big_tiles < 256) return 1;
         return 0;
