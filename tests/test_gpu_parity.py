@@ -510,10 +510,12 @@ def test_flash_attention_q8_0(bridge, oracle, D, M):
     assert torch.isfinite(O).all()
 
 
-@pytest.mark.parametrize("D,M", [(64, 1000), (128, 777)])
+@pytest.mark.parametrize("D,M", [(64, 1000), (64, 384), (64, 640), (128, 777)])
 def test_flash_attention_many_tiles(bridge, oracle, D, M):
-    """Many 64-key tiles per query block: the pipelined K/V staging (fetch one
-    tile ahead, two LDS buffers) across both unrolled halves and odd counts."""
+    """Many key tiles per query block: the pipelined K/V staging across tile
+    counts, the last partial tile, and (M = 384, 640: an odd number of
+    128-query tiles) the middle tile that pairs with itself, both wave groups
+    splitting every key tile of it and merging at the end."""
     H = 2
     rng = np.random.default_rng(D + M)
     Q, K, V = (rng.standard_normal((H, M, D)).astype(np.float16) for _ in range(3))
