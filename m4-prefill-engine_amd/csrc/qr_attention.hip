@@ -139,10 +139,12 @@ __device__ __forceinline__ void attn_stage_f16(const AttnRawF16<D>& raw, int tid
 // K / V through the same quantize-then-dequantize arithmetic as
 // quantize_q8_0_kernel + the Q8_0 path (bit-identical values), also writing
 // the Q8_0 blocks themselves to Kq / Vq when those are given -- the layer's
-// Q8_0 KV cache, produced in the same pass.  K units (one key's block) write K' rows straight out; V units
-// (a key pair's blocks) write {V[k][d], V[k+1][d]} words into an LDS tile
-// [d][key], whose rows then leave as 128-byte runs of V'^T.  Keys M .. Mp - 1
-// are zero.
+// Q8_0 KV cache, produced in the same pass.  Every output goes through LDS so
+// it leaves in contiguous runs: K units (one key's block) fill the tile's K'
+// rows (one contiguous 64-key run of K'); V units (a key pair's blocks) write
+// {V[k][d], V[k+1][d]} words into a tile [d][key] whose rows leave as 128-byte
+// runs of V'^T; the Q8_0 blocks of the tile's keys (contiguous in the cache)
+// leave as dword runs.  Keys M .. Mp - 1 are zero.
 template <bool FROM_Q8>
 __device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t w[16], uint8_t* q8out) {
     uint32_t d16, codes[8];  // code word c: codes of elements 4c .. 4c + 3
@@ -169,8 +171,8 @@ __device__ __forceinline__ void prep_block(const void* src, size_t blk, uint32_t
         quantize_block_q8_0(x, d16, c16);
 #pragma unroll
         for (int c = 0; c < 8; c++) codes[c] = c16[2 * c] | (c16[2 * c + 1] << 16);
-        if (q8out) {  // 34-byte blocks are 2-byte aligned
-            uint16_t* o16 = reinterpret_cast<uint16_t*>(q8out + blk * 34);
+        if (q8out) {  // this block's 34 bytes (2-byte aligned)
+            uint16_t* o16 = reinterpret_cast<uint16_t*>(q8out);
             o16[0] = (uint16_t)d16;
 #pragma unroll
             for (int i = 0; i < 16; i++) o16[1 + i] = (uint16_t)c16[i];
@@ -191,6 +193,12 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
     constexpr int TR = kBKV + 8;          // LDS row (halfs) of the transposed tile
     constexpr int KU = kBKV * NB, VU = (kBKV / 2) * NB;
     __shared__ __attribute__((aligned(16))) _Float16 T[D * TR];
+    constexpr int KR = D + 8;  // LDS row (halfs) of the K' tile
+    __shared__ __attribute__((aligned(16))) _Float16 KS[kBKV * KR];
+    // the tile's Q8_0 blocks (from fp16 input, when the cache is wanted):
+    // keys k0 .. k0 + 63 of K, then of V, 34-byte blocks back to back
+    constexpr int QB = kBKV * NB * 34;
+    __shared__ __attribute__((aligned(16))) uint8_t QS[FROM_Q8 ? 4 : 2 * QB];
     const int tid = threadIdx.x;
     const uint32_t k0 = blockIdx.x * kBKV, hk = blockIdx.y;
     const size_t head_blocks = (size_t)M * NB, head_dst = (size_t)Mp * D;
@@ -199,8 +207,10 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
             const int key = u % kBKV, db = u / kBKV;
             const uint32_t gk = k0 + key;
             uint32_t w[16] = {};
-            if (gk < M) prep_block<FROM_Q8>(Ksrc, hk * head_blocks + (size_t)gk * NB + db, w, Kq);
-            u4_t* dst = reinterpret_cast<u4_t*>(Kf + hk * head_dst + (size_t)gk * D + db * 32);
+            if (gk < M)
+                prep_block<FROM_Q8>(Ksrc, hk * head_blocks + (size_t)gk * NB + db, w,
+                                    (!FROM_Q8 && Kq) ? QS + (key * NB + db) * 34 : nullptr);
+            u4_t* dst = reinterpret_cast<u4_t*>(KS + key * KR + db * 32);
 #pragma unroll
             for (int c = 0; c < 4; c++) dst[c] = u4_t{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
         } else {
@@ -210,7 +220,9 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const uint32_t gk = k0 + 2 * kp + e;
-                if (gk < M) prep_block<FROM_Q8>(Vsrc, hk * head_blocks + (size_t)gk * NB + db, w[e], Vq);
+                if (gk < M)
+                    prep_block<FROM_Q8>(Vsrc, hk * head_blocks + (size_t)gk * NB + db, w[e],
+                                        (!FROM_Q8 && Vq) ? QS + QB + ((2 * kp + e) * NB + db) * 34 : nullptr);
             }
             uint32_t* t32 = reinterpret_cast<uint32_t*>(T);
 #pragma unroll
@@ -226,6 +238,38 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
         const int d = c / 8, kc = c % 8;
         *reinterpret_cast<u4_t*>(Vtf + hk * head_dst + (size_t)d * Mp + k0 + kc * 8) =
             *reinterpret_cast<const u4_t*>(T + d * TR + kc * 8);
+    }
+    for (int c = tid; c < kBKV * D / 8; c += 256) {  // the K' tile is one contiguous run
+        const int key = c / (D / 8), kc = c % (D / 8);
+        *reinterpret_cast<u4_t*>(Kf + hk * head_dst + (size_t)k0 * D + (size_t)c * 8) =
+            *reinterpret_cast<const u4_t*>(KS + key * KR + kc * 8);
+    }
+    if constexpr (!FROM_Q8) {
+        if (Kq) {  // the tile's blocks are one contiguous run of the cache (a multiple of 4 bytes)
+            const uint32_t nkeys = min((uint32_t)kBKV, M - k0);
+            const size_t first = (hk * head_blocks + (size_t)k0 * NB) * 34;
+            if (((reinterpret_cast<uintptr_t>(Kq) | reinterpret_cast<uintptr_t>(Vq)) & 3u) == 0) {
+                const int ndw = (int)(nkeys * NB * 34 / 4);
+                uint32_t* kd = reinterpret_cast<uint32_t*>(Kq + first);
+                uint32_t* vd = reinterpret_cast<uint32_t*>(Vq + first);
+                const uint32_t* ks = reinterpret_cast<const uint32_t*>(QS);
+                const uint32_t* vs = reinterpret_cast<const uint32_t*>(QS + QB);
+                for (int i = tid; i < ndw; i += 256) {
+                    kd[i] = ks[i];
+                    vd[i] = vs[i];
+                }
+            } else {  // caches only 2-byte aligned
+                const int nh = (int)(nkeys * NB * 17);
+                uint16_t* kd = reinterpret_cast<uint16_t*>(Kq + first);
+                uint16_t* vd = reinterpret_cast<uint16_t*>(Vq + first);
+                const uint16_t* ks = reinterpret_cast<const uint16_t*>(QS);
+                const uint16_t* vs = reinterpret_cast<const uint16_t*>(QS + QB);
+                for (int i = tid; i < nh; i += 256) {
+                    kd[i] = ks[i];
+                    vd[i] = vs[i];
+                }
+            }
+        }
     }
 }
 
