@@ -518,11 +518,14 @@ __global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(A
 // fp16 for the MFMA and for the row sums.
 // --------------------------------------------------------------------------
 constexpr int kPKV = 128;  // keys per tile of the pipelined kernel
+constexpr int kPVPad = 4;  // halfs of padding per V^T row of its LDS tiles
 
 template <int D>
 __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
     static_assert(D == 64, "chunk schedule and per-thread staging written for D = 64");
-    constexpr int KROW = D + 8, VROW = kPKV + 8, DT = D / 32;
+    // V^T rows of 132 halfs (66 dwords): the fragment reads of lanes j and
+    // j + 16 land 32 banks apart (a 68-dword row put them on the same banks)
+    constexpr int KROW = D + 8, VROW = kPKV + kPVPad, DT = D / 32;
     constexpr int NT = 512;
     constexpr int KT = kPKV * KROW, VT = D * VROW, TILE = KT + VT;
     constexpr int NBUF = 3;
@@ -575,7 +578,13 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
             const int c = tid + NT * i;
-            *reinterpret_cast<u4_t*>(vbuf(slot) + (c / (kPKV / 8)) * VROW + (c % (kPKV / 8)) * 8) = r.v[i];
+            _Float16* dst = vbuf(slot) + (c / (kPKV / 8)) * VROW + (c % (kPKV / 8)) * 8;
+            if constexpr (VROW % 8 == 0) {
+                *reinterpret_cast<u4_t*>(dst) = r.v[i];
+            } else {  // rows 8-byte aligned only
+                reinterpret_cast<u2_t*>(dst)[0] = u2_t{r.v[i].x, r.v[i].y};
+                reinterpret_cast<u2_t*>(dst)[1] = u2_t{r.v[i].z, r.v[i].w};
+            }
         }
     };
 
@@ -863,7 +872,7 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
         store(l > 0.0f ? 1.0f / l : 0.0f);
     }
 }
-constexpr size_t kPipeLds = 3 * (size_t)(kPKV * (64 + 8) + 64 * (kPKV + 8)) * 2;
+constexpr size_t kPipeLds = 3 * (size_t)(kPKV * (64 + 8) + 64 * (kPKV + kPVPad)) * 2;
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
