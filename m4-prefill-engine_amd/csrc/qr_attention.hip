@@ -880,13 +880,9 @@ hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     if (p.Kf == nullptr || p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV) return hipErrorInvalidValue;
     if (p.D == 64) {
         const uint32_t qtiles = (p.M + kBQ - 1) / kBQ;
-        static bool attr = false;  // the 3-tile ring needs more than the default 64 KB of LDS
-        if (!attr) {
-            const hipError_t e = hipFuncSetAttribute((const void*)flash_attn_pipe_kernel<64>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPipeLds);
-            if (e != hipSuccess) return e;
-            attr = true;
-        }
+        static size_t attr[kMaxDevices] = {};  // the 3-tile ring needs more than the default 64 KB of LDS
+        const hipError_t e = lds_limit_once((const void*)flash_attn_pipe_kernel<64>, kPipeLds, attr);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL((flash_attn_pipe_kernel<64>), dim3(((qtiles + 1) / 2) * p.H), dim3(512), kPipeLds, st, p);
         return hipGetLastError();
     }

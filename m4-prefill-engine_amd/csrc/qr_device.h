@@ -114,4 +114,19 @@ __device__ __forceinline__ uint32_t affine_pair_any(h2_t q, float A, float C, bo
     return lo | (hi << 16);
 }
 
+
+// Raises a kernel's dynamic-LDS limit to `bytes` once per device (HIP function
+// attributes are per device); `done` is the caller's per-kernel record.
+constexpr int kMaxDevices = 64;
+inline hipError_t lds_limit_once(const void* kern, size_t bytes, size_t (&done)[kMaxDevices]) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    if (done[dev] >= bytes) return hipSuccess;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) done[dev] = bytes;
+    return e;
+}
+
 }  // namespace qr

@@ -417,14 +417,11 @@ static hipError_t launch_sk(const GemmParams& p, float* ws, uint32_t ks, hipStre
     auto kern = gemm_skinny_kernel<F, MT, GPW>;
     const uint32_t groups = (p.N + kSkCols - 1) / kSkCols;
     const size_t lds = sk_layout(p.M, GPW, GroupBytes<F>::v).lds;
-    static size_t attr = 0;  // dynamic LDS limit set for this instantiation
-    if (lds > attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr = lds;
-    }
+    static size_t attr[kMaxDevices] = {};  // dynamic LDS limit set for this instantiation, per device
+    hipError_t e = lds_limit_once((const void*)kern, lds, attr);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(groups, ks), dim3(kSkThreads), lds, st, p, ws, ks);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e == hipSuccess && ks > 1) e = launch_splitk_reduce(ws, ks, p.M, p.N, false, p.R, p.Y, p.head_D, st);
     return e;
     }
