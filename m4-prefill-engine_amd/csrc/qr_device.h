@@ -98,12 +98,12 @@ __device__ __forceinline__ h2_t code_pair(uint32_t bytes) {
 constexpr float kQ4_0FastMaxScale = 8188.0f;
 
 // RNE binary16 of q*A + C for both codes of a pair, when q*A + C is exact in
-// fp32 (fused fp32 fma of the fp16 code, one rounding to fp16; maps to
-// v_fma_mix{lo,hi}_f16).
+// fp32 (fused fp32 fma of the fp16 code, one rounding to fp16).  Built as a
+// half2 vector so the pair is one v_fma_mixlo_f16 + one v_fma_mixhi_f16 into
+// the same register (two separate halves cost a shift and an OR more).
 __device__ __forceinline__ uint32_t affine_pair_exact(h2_t q, float A, float C) {
-    const _Float16 lo = (_Float16)__builtin_fmaf((float)q.x, A, C);
-    const _Float16 hi = (_Float16)__builtin_fmaf((float)q.y, A, C);
-    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    const h2_t r = {(_Float16)__builtin_fmaf((float)q.x, A, C), (_Float16)__builtin_fmaf((float)q.y, A, C)};
+    return __builtin_bit_cast(uint32_t, r);
 }
 
 // Same for any inputs: the exact-sum (round-to-odd) path where `exact` is false.

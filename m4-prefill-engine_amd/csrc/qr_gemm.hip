@@ -275,15 +275,25 @@ gemm_rb_kernel(GemmParams p) {
         }
         if constexpr (F == QUANT_Q4_K || F == QUANT_Q4_0) {
             // wave-uniform slow path: re-decode exactly when any lane's group
-            // needs it (Q4_K binade gap; Q4_0 scales with -8 d not finite)
-            bool slow = false;
+            // needs it (Q4_K binade gap; Q4_0 scales with -8 d not finite).
+            // The exact words replace the fast ones per lane through a select,
+            // so the fast words stay live on both paths: overwritten outright,
+            // the compiler sinks the fast decode into the not-slow branch,
+            // behind the step's MFMAs, where it no longer issues under them.
+            bool slow[NCB], any_slow = false;
 #pragma unroll
-            for (int jb = 0; jb < NCB; jb++)
-                slow |= needs_exact<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn));
-            if (__any(slow)) {
+            for (int jb = 0; jb < NCB; jb++) {
+                slow[jb] = needs_exact<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn));
+                any_slow |= slow[jb];
+            }
+            if (__any(any_slow)) {
 #pragma unroll
-                for (int jb = 0; jb < NCB; jb++)
-                    decode_group<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn), bn[jb]);
+                for (int jb = 0; jb < NCB; jb++) {
+                    uint32_t ex[16];
+                    decode_group<F>(wraw[wslot][jb], Dec::parity((uint32_t)bcol(jb) * col_bytes, gn), ex);
+#pragma unroll
+                    for (int w = 0; w < 16; w++) bn[jb][w] = slow[jb] ? ex[w] : bn[jb][w];
+                }
             }
         }
         load_w(s + 1 + WP, wslot);

@@ -296,6 +296,40 @@ def test_gemm_q4_0_scales_beyond_fast_path(bridge, oracle):
     tolerance.check(host(Y), ref, tolerance.gemm_bound(ref, absxw(oracle, 0, X, W, K, N), K))
 
 
+@pytest.mark.parametrize("fmt", [0, 2])
+@pytest.mark.parametrize("M,K,N", [(256, 512, 256), (1024, 1024, 256)])
+def test_gemm_decode_bit_exact_mixed_exact_paths(bridge, oracle, fmt, M, K, N):
+    """The tiled kernel's weight decode, bit for bit, with the exact-decode
+    path taken by some lanes of a wave and not others: about a third of the
+    Q4_0 blocks have |d| > 8188 (-8 d not finite) and a third of the Q4_K
+    super-blocks a binade gap between d and dmin above 3.  X is one-hot
+    (row m selects k = m mod K), so every output is one exact product and
+    Y[m, n] must equal the CPU unpack of W[n, m mod K]."""
+    rng = np.random.default_rng(300 + fmt + M)
+    if fmt == 0:
+        W = synth.random_blocks(0, N, K, 301).reshape(N, K // 32, 18).copy()
+        big = rng.random((N, K // 32)) < 0.35
+        d = (rng.random((N, K // 32)) * 800 + 8190) * np.where(rng.random((N, K // 32)) < 0.5, -1, 1)
+        W[big, 0:2] = d[big].astype(np.float16)[..., None].view(np.uint8)
+        codes = (rng.integers(1, 16, (N, K // 32, 16)) | (rng.integers(1, 16, (N, K // 32, 16)) << 4)).astype(np.uint8)
+        W[big, 2:] = codes[big]
+    else:
+        W = synth.random_blocks(2, N, K, 302).reshape(N, K // 256, 144).copy()
+        gap = rng.random((N, K // 256)) < 0.35
+        W[gap, 0:2] = np.float16(3.0).reshape(1).view(np.uint8)
+        W[gap, 2:4] = (rng.random(int(gap.sum())) * 1e-4 + 1e-5).astype(np.float16)[..., None].view(np.uint8)
+    W = W.reshape(-1)
+    X = np.zeros((M, K), np.float16)
+    X[np.arange(M), np.arange(M) % K] = 1.0
+    Y = empty16(M, N)
+    bridge.dispatch_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    wd = oracle.dequantize(fmt, W, K, N).astype(np.float32)  # [N, K]
+    assert np.isfinite(wd).all()
+    # +0 and -0 compare equal: the fast Q4_0 decode gives +0 where the CPU unpack gives -0
+    np.testing.assert_array_equal(host(Y).astype(np.float32), wd[:, np.arange(M) % K].T)
+
+
 @pytest.mark.parametrize("fmt", [6, 7])
 @pytest.mark.parametrize("M,K,N", [(1, 384, 256), (33, 384, 200), (129, 512, 256), (128, 4096, 320),
                                    (300, 1152, 136)])
