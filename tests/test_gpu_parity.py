@@ -330,6 +330,37 @@ def test_gemm_decode_bit_exact_mixed_exact_paths(bridge, oracle, fmt, M, K, N):
     np.testing.assert_array_equal(host(Y).astype(np.float32), wd[:, np.arange(M) % K].T)
 
 
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3, 8])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (33, 4096, 4104), (64, 2048, 4096), (17, 1024, 4096)])
+def test_gemm_small_m_wide(bridge, oracle, fmt, M, K, N):
+    """The small-M projection (M <= 64) on wide outputs, every format it
+    takes (config 1's shape is (33, 4096, 4096)): standard, residual and
+    direct-head outputs against the oracle on sampled rows; N = 4104 leaves a
+    ragged last column strip; runs are bit-identical (fixed-order split-K)."""
+    rng = np.random.default_rng(500 + fmt + M)
+    X = synth.activations(M, K, 501 + M, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 502 + fmt)
+    R = synth.activations(M, N, 503)
+    Y, Y2, Yr = empty16(M, N), empty16(M, N), empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y2, fmt, M, K, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    D = 64
+    Yh = empty16(N // D, M, D) if N % D == 0 else None
+    if Yh is not None:
+        bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, N // D, D, K)
+    bridge.synchronize()
+    rows = np.unique(np.r_[0, M - 1, rng.integers(0, M, 3)])
+    Xs = np.ascontiguousarray(X[rows])
+    gold = oracle.gemm(fmt, Xs, W, N)
+    tolerance.check_ref(host(Y)[rows], gold, what=f"fmt {fmt} {M}x{K}x{N}")
+    np.testing.assert_array_equal(host(Y2).view(np.uint16), host(Y).view(np.uint16))
+    tolerance.check_ref(host(Yr)[rows], oracle.gemm(fmt, Xs, W, N, R=np.ascontiguousarray(R[rows])), what="residual")
+    if Yh is not None:  # [H, M, D]: the sampled rows of every head
+        np.testing.assert_array_equal(host(Yh)[:, rows, :].transpose(1, 0, 2).reshape(len(rows), N).view(np.uint16),
+                                      host(Y)[rows].view(np.uint16))
+
+
 @pytest.mark.parametrize("fmt", [6, 7])
 @pytest.mark.parametrize("M,K,N", [(1, 384, 256), (33, 384, 200), (129, 512, 256), (128, 4096, 320),
                                    (300, 1152, 136)])
