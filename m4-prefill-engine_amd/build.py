@@ -17,8 +17,8 @@ OUT = HERE / "libm4_bridge.so"
 BUILD = HERE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# (source, object stem, extra defines).  The tiled projection kernel is built
-# once per format (0..7) so its instantiations compile in parallel.
+# (source, object stem, extra flags).  The tiled projection kernel is built
+# once per format (0..8) so its instantiations compile in parallel.
 SOURCES = ([("qr_gemm.hip", f"qr_gemm_f{f}", (f"-DQR_GEMM_FORMAT={f}",)) for f in range(9)] +
            [(s, s.rsplit(".", 1)[0], ()) for s in ("qr_gemm_host.hip", "qr_gemm_skinny.hip", "qr_dequant.hip",
                                                    "qr_attention.hip", "qr_norm_rope.hip", "qr_probe.hip", "qr_bridge.cpp", "qr_registry.cpp",
@@ -37,7 +37,7 @@ def _fresh(obj: Path, src: str) -> bool:
     if not obj.exists():
         return False
     t = obj.stat().st_mtime
-    deps = [CSRC / src, *CSRC.glob("*.h"), *(HERE.parent / "include").glob("*.h")]
+    deps = [CSRC / src, *CSRC.glob("*.h"), *(HERE.parent / "include").glob("*.h"), HERE / "build.py"]
     return all(d.stat().st_mtime < t for d in deps)
 
 
