@@ -164,6 +164,48 @@ def bench_projection(b, timer, name, fmt, M, K, N, seed):
     }, (Xn, Wn)
 
 
+def bench_host_buffers(b, name, fmt, M, K, N, seed, calls: int = 10):
+    """The headline projection with host buffers (the reference's callers pass
+    unified-memory host pointers): every call copies X and W in over PCIe,
+    runs, and copies Y back at synchronize.  Eager, wall-clock per call; this
+    is the PCIe-inclusive rate, never `value`.  Pageable (numpy) and pinned
+    (torch pin_memory) host memory."""
+    import torch
+
+    import synth
+
+    Xn = synth.activations(M, K, seed)
+    Wn = synth.quantized_weights(fmt, N, K, seed + 1)
+    out = {"name": name, "format": fmt, "M": M, "K": K, "N": N, "calls": calls}
+    bytes_ = Xn.nbytes + Wn.nbytes + M * N * 2
+    for kind in ("pageable", "pinned"):
+        if kind == "pageable":
+            X, W, Y = Xn, Wn, np.empty((M, N), np.float16)
+            ptr = lambda a: a.ctypes.data  # noqa: E731
+        else:
+            X = torch.from_numpy(Xn).pin_memory()
+            W = torch.from_numpy(Wn).pin_memory()
+            Y = torch.empty(M, N, dtype=torch.float16).pin_memory()
+            ptr = lambda a: a.data_ptr()  # noqa: E731
+        xp, wp, yp = ptr(X), ptr(W), ptr(Y)
+
+        def call():
+            check(b.lib.m4_bridge_dispatch_gemm(xp, Xn.nbytes, wp, Wn.nbytes, yp, M * N * 2, fmt, M, K, N), name)
+            b.lib.m4_bridge_synchronize()
+
+        for _ in range(2):
+            call()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            call()
+        ms = (time.perf_counter() - t0) * 1e3 / calls
+        out[f"{kind}_ms"] = round(ms, 4)
+        out[f"{kind}_gbs"] = round(bytes_ / (ms * 1e-3) / 1e9, 1)
+        out[f"{kind}_tflops"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
+    out["bytes_over_pcie"] = bytes_
+    return out
+
+
 def bench_swiglu(b, timer, M, K, N, seed):
     import torch
 
@@ -460,6 +502,8 @@ def main():
                             ("ref_fp16_gemm_m2048_k4096_n4096", (2048, 4096, 4096))):
         if on(name):
             per[name] = bench_fp16_reference(timer, name, M, K, N)
+    if on("cfg2_host_buffers"):
+        per["cfg2_host_buffers"] = bench_host_buffers(b, "cfg2_host_buffers", 1, 128, 4096, 14336, 20)
     if want is not None and "copy_calib" in want:
         per["copy_calib"] = bench_copy(timer, 256 << 20)
     if on("cfg5_swiglu"):

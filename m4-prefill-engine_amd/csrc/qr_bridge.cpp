@@ -41,9 +41,52 @@ struct Staged {
     void* host;      // non-null: copy dev -> host at synchronize (once armed)
     size_t bytes;
     bool armed;      // set once the dispatch that staged it has launched its kernels
+    size_t cap;      // bytes of the staging allocation (>= bytes)
 };
-std::vector<Staged> g_staged;      // freed at synchronize
+std::vector<Staged> g_staged;      // returned to the staging pool at synchronize
 size_t g_staged_bytes = 0;
+
+// Staging allocations are reused: synchronize returns them to this free list
+// and the next staged buffer takes the smallest one that fits, so a caller
+// that passes host (or misaligned) buffers on every call allocates only while
+// its working set grows.  The list keeps at most kPoolMaxBytes; beyond that
+// the largest free allocations are released.
+std::vector<std::pair<void*, size_t>> g_pool;
+size_t g_pool_bytes = 0;
+constexpr size_t kPoolMaxBytes = size_t(4) << 30;
+
+hipError_t pool_take(size_t bytes, void** out, size_t* cap) {
+    int best = -1;
+    for (int i = 0; i < (int)g_pool.size(); i++)
+        if (g_pool[i].second >= bytes && (best < 0 || g_pool[i].second < g_pool[best].second)) best = i;
+    if (best >= 0) {
+        *out = g_pool[best].first;
+        *cap = g_pool[best].second;
+        g_pool_bytes -= *cap;
+        g_pool.erase(g_pool.begin() + best);
+        return hipSuccess;
+    }
+    // whole MiB above 1 MiB, powers of two below: sizes that later calls reuse
+    size_t c = 256;
+    if (bytes > (size_t(1) << 20)) c = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    else
+        while (c < bytes) c <<= 1;
+    *cap = c;
+    return hipMalloc(out, c);
+}
+
+void pool_give(void* p, size_t cap) {
+    g_pool.emplace_back(p, cap);
+    g_pool_bytes += cap;
+    while (g_pool_bytes > kPoolMaxBytes) {
+        size_t big = 0;
+        for (size_t i = 1; i < g_pool.size(); i++)
+            if (g_pool[i].second > g_pool[big].second) big = i;
+        (void)hipFree(g_pool[big].first);
+        g_pool_bytes -= g_pool[big].second;
+        g_pool.erase(g_pool.begin() + big);
+    }
+}
 
 // Grow-only scratch for the layer composition, and for the dequantized fp16
 // K / V^T cache of the standalone attention entry points.
@@ -176,7 +219,8 @@ void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
     }
     if (!d && in) flush_pending_host_outputs(p, bytes);
     void* s = nullptr;
-    hipError_t e = hipMalloc(&s, bytes ? bytes : 16);
+    size_t cap = 0;
+    hipError_t e = pool_take(bytes ? bytes : 16, &s, &cap);
     if (e != hipSuccess) {
         set_error("hipMalloc(staging)", e);
         return nullptr;
@@ -186,13 +230,13 @@ void* resolve(void* p, size_t bytes, size_t align, bool in, bool out) {
               : hipMemcpyAsync(s, p, bytes, hipMemcpyHostToDevice, g_stream);
         if (e != hipSuccess) {
             set_error("hipMemcpyAsync(stage in)", e);
-            (void)hipFree(s);
+            pool_give(s, cap);
             return nullptr;
         }
     }
     // Device outputs that were only misaligned are copied back on the stream
     // right after the kernel (see finish_outputs); host outputs at synchronize.
-    g_staged.push_back({s, out ? p : nullptr, bytes, false});
+    g_staged.push_back({s, out ? p : nullptr, bytes, false, cap});
     g_staged_bytes += bytes;
     return s;
 }
@@ -241,7 +285,7 @@ void sync_and_release() {
             e = hipMemcpy(st.host, st.dev, st.bytes, hipMemcpyDeviceToHost);
             if (e != hipSuccess) set_error("hipMemcpy(stage out)", e);
         }
-        (void)hipFree(st.dev);
+        pool_give(st.dev, st.cap);
     }
     g_staged.clear();
     g_staged_bytes = 0;
@@ -829,7 +873,7 @@ double m4_bridge_get_uma_footprint_mb(void) {
         fclose(f);
     }
     double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
-    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_sk_ws_floats * 4 +
+    return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_pool_bytes + g_sk_ws_floats * 4 +
                               g_retired_bytes) /
                          (1024.0 * 1024.0);
 }
@@ -852,6 +896,9 @@ void m4_bridge_shutdown(void) {
     if (g_sk_ws) (void)hipFree(g_sk_ws);
     for (void* r : g_retired) (void)hipFree(r);
     g_retired.clear();
+    for (auto& b : g_pool) (void)hipFree(b.first);
+    g_pool.clear();
+    g_pool_bytes = 0;
     g_retired_bytes = 0;
     g_sk_ws = nullptr;
     g_sk_ws_floats = 0;
