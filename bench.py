@@ -424,7 +424,8 @@ def traffic_from_profile(name: str):
 
 def probes(b):
     """On-device ceilings (the reference's roofline probes): HBM read and copy
-    GB/s over 1 GiB, dense fp16 MFMA TFLOP/s and the clock it ran at."""
+    GB/s over 1 GiB, dense fp16 MFMA TFLOP/s and the clock it ran at, with
+    low-entropy and with random operands."""
     import ctypes
 
     r, c, t, g = (ctypes.c_double() for _ in range(4))
@@ -435,6 +436,10 @@ def probes(b):
     if b.lib.m4_probe_mfma_f16(4096, 5, ctypes.byref(t), ctypes.byref(g)) == 0:
         out.update(mfma_f16_tflops=round(t.value, 1), mfma_clock_ghz=round(g.value, 3),
                    mfma_frac_of_peak=round(t.value / PEAK_MFMA_TFLOPS, 4))
+    # random operands: the ceiling real data reaches (power-limited clock)
+    if b.lib.m4_probe_mfma_f16_random(4096, 5, ctypes.byref(t), ctypes.byref(g)) == 0:
+        out.update(mfma_f16_random_tflops=round(t.value, 1), mfma_random_clock_ghz=round(g.value, 3),
+                   mfma_random_frac_of_peak=round(t.value / PEAK_MFMA_TFLOPS, 4))
     return out
 
 

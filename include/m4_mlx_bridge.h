@@ -239,8 +239,15 @@ M4_API int m4_probe_hbm_bandwidth(size_t bytes, int reps, double* read_gbs, doub
 /* probe_fma_roofline, on the matrix pipe: dense fp16 TFLOP/s of back-to-back
  * v_mfma_f32_32x32x16_f16 on every SIMD (`iters` rounds of 4 independent
  * chains per wave), best of `reps`, and the average shader clock (GHz) the
- * waves saw (shader-cycle counter over the 100 MHz real-time counter). */
+ * waves saw (shader-cycle counter over the 100 MHz real-time counter).
+ * `iters` >= 64 and a multiple of 4.  0, -2, -4 or -6. */
 M4_API int m4_probe_mfma_f16(uint32_t iters, int reps, double* tflops, double* clock_ghz);
+/* The same with random fp16 operands (four A and four B fragments per lane,
+ * values in [-1, 1)): the matrix pipe draws more power when more operand bits
+ * toggle, and the part lowers its clock, so this is the dense ceiling real
+ * activations and weights can reach.  No counterpart in the reference (its
+ * FMA probe is operand-independent).  `iters` a multiple of 4.  0, -2, -4, -6. */
+M4_API int m4_probe_mfma_f16_random(uint32_t iters, int reps, double* tflops, double* clock_ghz);
 
 /* ---- format registry (src/router/quant_registry.h:14-65) ---------------- */
 

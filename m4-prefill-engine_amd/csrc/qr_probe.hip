@@ -50,22 +50,46 @@ __global__ void __launch_bounds__(256) probe_copy_kernel(const f4_t* __restrict_
 // instruction's latency, for `iters` rounds.  Thread 0 of every workgroup
 // records the shader-clock and constant 100 MHz counters around the loop, so
 // the host can report the clock the matrix pipe ran at.
+// RND = false: the same low-entropy operands every round (near 1.0 and powers
+// of two); RND = true: every lane cycles through four random fp16 A and four
+// B fragments from `tab` (values in [-1, 1)).  The matrix pipe's power, and
+// with it the clock the part holds, depends on how many operand bits toggle,
+// so the random form is the ceiling real activations and weights can reach.
 constexpr int kChains = 4;
+template <bool RND>
 __global__ void __launch_bounds__(256) probe_mfma_kernel(float* __restrict__ out, uint32_t iters,
-                                                         unsigned long long* __restrict__ clocks) {
+                                                         unsigned long long* __restrict__ clocks,
+                                                         const h8_t* __restrict__ tab) {
     const int lane = threadIdx.x & 63;
-    const _Float16 v = (_Float16)(1.0f + 0.001f * (float)(lane & 7));
-    const h8_t a = {v, v, v, v, v, v, v, v};
-    const h8_t b = {(_Float16)0.5f, (_Float16)0.25f, (_Float16)0.125f, (_Float16)0.5f,
+    h8_t a[4], b[4];
+    if constexpr (RND) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            a[i] = tab[threadIdx.x * 8 + i];
+            b[i] = tab[threadIdx.x * 8 + 4 + i];
+        }
+    } else {
+        const _Float16 v = (_Float16)(1.0f + 0.001f * (float)(lane & 7));
+        a[0] = h8_t{v, v, v, v, v, v, v, v};
+        b[0] = h8_t{(_Float16)0.5f, (_Float16)0.25f, (_Float16)0.125f, (_Float16)0.5f,
                     (_Float16)0.25f, (_Float16)0.125f, (_Float16)0.5f, (_Float16)0.25f};
+#pragma unroll
+        for (int i = 1; i < 4; i++) {
+            a[i] = a[0];
+            b[i] = b[0];
+        }
+    }
     f16v_t acc[kChains];
 #pragma unroll
     for (int c = 0; c < kChains; c++) acc[c] = f16v_t{};
     const unsigned long long c0 = __builtin_readcyclecounter();
     const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
-    for (uint32_t it = 0; it < iters; it++) {
+    for (uint32_t it = 0; it < iters; it += 4) {  // iters is a multiple of 4
 #pragma unroll
-        for (int c = 0; c < kChains; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int c = 0; c < kChains; c++)
+                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[(u + c) & 3], b[(3 * u + c) & 3], acc[c], 0, 0, 0);
     }
     float s = 0.0f;
 #pragma unroll
@@ -142,9 +166,9 @@ int m4_probe_hbm_bandwidth(size_t bytes, int reps, double* read_gbs, double* cop
     return 0;
 }
 
-int m4_probe_mfma_f16(uint32_t iters, int reps, double* tflops, double* clock_ghz) {
+static int probe_mfma(bool rnd, uint32_t iters, int reps, double* tflops, double* clock_ghz) {
     if (!tflops || !clock_ghz) return -2;
-    if (iters < 64 || reps < 1) return -4;
+    if (iters < 64 || iters % 4 || reps < 1) return -4;
     hipDeviceProp_t prop;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -152,16 +176,34 @@ int m4_probe_mfma_f16(uint32_t iters, int reps, double* tflops, double* clock_gh
     if (e != hipSuccess) return -6;
     // four waves per CU (one per SIMD) of 4 independent chains each, 8x over
     const int blocks = prop.multiProcessorCount * 8;
-    void *out = nullptr, *clk = nullptr;
+    void *out = nullptr, *clk = nullptr, *tab = nullptr;
     e = hipMalloc(&out, (size_t)blocks * 256 * 4);
     if (e == hipSuccess) e = hipMalloc(&clk, (size_t)blocks * 16);
+    if (e == hipSuccess && rnd) {  // 8 fragments per thread of a 256-thread block, fixed LCG
+        const size_t n = 256 * 8 * 8;
+        _Float16* h = new _Float16[n];
+        uint32_t x = 12345u;
+        for (size_t i = 0; i < n; i++) {
+            x = x * 1664525u + 1013904223u;
+            h[i] = (_Float16)((float)(x >> 8) * (2.0f / 16777216.0f) - 1.0f);
+        }
+        e = hipMalloc(&tab, n * 2);
+        if (e == hipSuccess) e = hipMemcpy(tab, h, n * 2, hipMemcpyHostToDevice);
+        delete[] h;
+    }
     Events ev;
     float best = 1e30f;
     for (int r = 0; r < reps + 1 && e == hipSuccess; r++) {
         float ms = 0.0f;
         (void)hipEventRecord(ev.a, nullptr);
-        hipLaunchKernelGGL(qr::probe_mfma_kernel, dim3(blocks), dim3(256), 0, nullptr, static_cast<float*>(out),
-                           iters, static_cast<unsigned long long*>(clk));
+        if (rnd)
+            hipLaunchKernelGGL(qr::probe_mfma_kernel<true>, dim3(blocks), dim3(256), 0, nullptr,
+                               static_cast<float*>(out), iters, static_cast<unsigned long long*>(clk),
+                               static_cast<const qr::h8_t*>(tab));
+        else
+            hipLaunchKernelGGL(qr::probe_mfma_kernel<false>, dim3(blocks), dim3(256), 0, nullptr,
+                               static_cast<float*>(out), iters, static_cast<unsigned long long*>(clk),
+                               static_cast<const qr::h8_t*>(tab));
         (void)hipEventRecord(ev.b, nullptr);
         e = hipEventSynchronize(ev.b);
         if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.a, ev.b);
@@ -181,11 +223,20 @@ int m4_probe_mfma_f16(uint32_t iters, int reps, double* tflops, double* clock_gh
     }
     if (out) (void)hipFree(out);
     if (clk) (void)hipFree(clk);
+    if (tab) (void)hipFree(tab);
     if (e != hipSuccess) return -6;
     const double flop = (double)blocks * 4 /* waves */ * qr::kChains * iters * (32.0 * 32.0 * 16.0 * 2.0);
     *tflops = flop / (best * 1e-3) / 1e12;
     *clock_ghz = ghz;
     return 0;
+}
+
+int m4_probe_mfma_f16(uint32_t iters, int reps, double* tflops, double* clock_ghz) {
+    return probe_mfma(false, iters, reps, tflops, clock_ghz);
+}
+
+int m4_probe_mfma_f16_random(uint32_t iters, int reps, double* tflops, double* clock_ghz) {
+    return probe_mfma(true, iters, reps, tflops, clock_ghz);
 }
 
 }  // extern "C"

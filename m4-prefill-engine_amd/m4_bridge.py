@@ -90,6 +90,7 @@ SIGNATURES = {
     "m4_bridge_last_error": ([], ctypes.c_char_p),
     "m4_probe_hbm_bandwidth": ([_SZ, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], _I),
     "m4_probe_mfma_f16": ([_U32, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], _I),
+    "m4_probe_mfma_f16_random": ([_U32, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], _I),
     "m4_registry_get": ([_I, _VP], _I),
     "m4_registry_get_by_name": ([ctypes.c_char_p], _I),
     "m4_registry_available_formats": ([ctypes.POINTER(_I), _I], _I),

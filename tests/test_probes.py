@@ -33,6 +33,9 @@ def test_probe_arguments_are_checked_before_device_work(lib):
     assert lib.m4_probe_mfma_f16(4096, 1, ctypes.byref(t), None) == -2
     assert lib.m4_probe_mfma_f16(16, 1, ctypes.byref(t), ctypes.byref(g)) == -4  # fewer than 64 rounds
     assert lib.m4_probe_mfma_f16(4096, 0, ctypes.byref(t), ctypes.byref(g)) == -4
+    assert lib.m4_probe_mfma_f16_random(4096, 1, None, ctypes.byref(g)) == -2
+    assert lib.m4_probe_mfma_f16_random(4098, 1, ctypes.byref(t), ctypes.byref(g)) == -4  # not a multiple of 4
+    assert lib.m4_probe_mfma_f16_random(16, 1, ctypes.byref(t), ctypes.byref(g)) == -4
 
 
 @pytest.mark.gpu
@@ -48,3 +51,8 @@ def test_probes_measure_plausible_ceilings(bridge):
     assert lib.m4_probe_mfma_f16(1024, 2, ctypes.byref(t), ctypes.byref(g)) == 0
     assert 100.0 < t.value < 2500.0, t.value   # TFLOP/s, below the dense fp16 peak
     assert 0.5 < g.value < 3.0, g.value        # GHz
+    tr, gr = ctypes.c_double(), ctypes.c_double()
+    print("probe: mfma random operands 1024 rounds x 2", flush=True)
+    assert lib.m4_probe_mfma_f16_random(1024, 2, ctypes.byref(tr), ctypes.byref(gr)) == 0
+    assert 100.0 < tr.value < 2500.0, tr.value
+    assert 0.5 < gr.value < 3.0, gr.value
