@@ -411,6 +411,23 @@ class HIPBridge:
         self._in_flight_tensors.append(bufs)
         return ret
 
+    def prefill_layer_ex_kv(self, X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, X_out, Kq_out, Vq_out, format, M,
+                            d_model, Hq, Hkv, D, N_mlp, attn_scale, norm_type: int = 1, norm_eps: float = 1e-5,
+                            rope: bool = True, rope_theta: float = 10000.0, rope_offset: int = 0,
+                            rope_traditional: bool = False) -> int:
+        """prefill_layer_ex that also writes the layer's Q8_0 K / V cache
+        (unified_prefill_engine.mm:548-572) to Kq_out / Vq_out."""
+        bufs = (X, w_attn, Wq, Wk, Wv, Wo, w_ffn, Wg, Wu, Wd, X_out, Kq_out, Vq_out)
+        ptrs = [None if t is None else self.extract_buffer_address_and_size(t)[0] for t in bufs]
+        self._bind_stream(*[t for t in bufs if t is not None])
+        ret = self._lib.m4_bridge_prefill_layer_ex_kv(*ptrs, int(format), M, d_model, Hq, Hkv, D, N_mlp,
+                                                      float(attn_scale), int(norm_type), float(norm_eps),
+                                                      int(bool(rope)), float(rope_theta), int(rope_offset),
+                                                      int(bool(rope_traditional)))
+        self._check("m4_bridge_prefill_layer_ex_kv", ret)
+        self._in_flight_tensors.append(bufs)
+        return ret
+
     def dequantize(self, W, out, format, K, N) -> int:
         a = [self.extract_buffer_address_and_size(t) for t in (W, out)]
         self._bind_stream(W, out)
