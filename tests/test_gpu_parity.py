@@ -455,6 +455,45 @@ def test_bridge_basic_known_answers_host_buffers(bridge):
     assert np.all(y == K)
 
 
+def test_host_staging_buffers_are_reused(bridge):
+    """Host (numpy) buffers of changing sizes, several dispatches per
+    synchronize: every output equals the device-resident dispatch bit for bit,
+    and once the working set is reached repeated calls allocate no more
+    staging memory (the free list refilled at synchronize is reused)."""
+    import torch
+
+    shapes = [(64, 512, 256), (130, 1024, 512), (64, 512, 256), (33, 4096, 4096), (130, 1024, 512)]
+    inputs = []
+    for i, (M, K, N) in enumerate(shapes):
+        X = synth.activations(M, K, 700 + i)
+        W = synth.quantized_weights(0, N, K, 710 + i)
+        Yd = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        bridge.dispatch_gemm(dev(X), dev(W), Yd, 0, M, K, N)
+        inputs.append((X, W, host(Yd)))
+    bridge.synchronize()
+    for rnd in range(2):
+        outs = []
+        for (M, K, N), (X, W, _) in zip(shapes, inputs):
+            Y = np.zeros((M, N), np.float16)
+            bridge.dispatch_gemm(X, W, Y, 0, M, K, N)
+            outs.append(Y)
+        bridge.synchronize()
+        for Y, (_, _, Yref) in zip(outs, inputs):
+            np.testing.assert_array_equal(Y.view(np.uint16), Yref.view(np.uint16))
+    # the largest call again and again: the footprint (host RSS + device memory
+    # the bridge holds) stays within a few MB, far below one call's 9.7 MB of staging
+    X, W, _ = inputs[3]
+    Y = np.zeros((33, 4096), np.float16)
+    bridge.dispatch_gemm(X, W, Y, 0, 33, 4096, 4096)
+    bridge.synchronize()
+    before = bridge.get_uma_footprint_mb()
+    for _ in range(20):
+        bridge.dispatch_gemm(X, W, Y, 0, 33, 4096, 4096)
+        bridge.synchronize()
+    assert bridge.get_uma_footprint_mb() - before < 4.0
+    np.testing.assert_array_equal(Y.view(np.uint16), inputs[3][2].view(np.uint16))
+
+
 def test_gemv_and_misaligned_pointers(bridge, oracle):
     import torch
 
