@@ -531,7 +531,7 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
     constexpr int KROW = D + 8, VROW = kPKV + kPVPad, DT = D / 32;
     constexpr int NT = 512;
     constexpr int KT = kPKV * KROW, VT = D * VROW, TILE = KT + VT;
-    constexpr int NBUF = 3;
+    constexpr int NBUF = 4;
     constexpr int KCH = kPKV * (D / 8) / NT, VCH = D * (kPKV / 8) / NT;  // 16-byte chunks per thread
     extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
 
@@ -593,16 +593,13 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
 
     // ---- this wave's units (key start 32 * unit index within the keys):
     // segment 1 = units 0..3 of tiles [0, Tl) (light queries for group 0,
-    // heavy for group 1), segment 2 = units 2 grp, 2 grp + 1 of tiles
-    // [Tl, Th) (heavy queries); each segment keeps the prefix whose first key
-    // is at or below the wave's last query ----
+    // heavy for group 1); segment 2 = tiles [Tl, Th) on the heavy queries, in
+    // pairs (group 0 the first tile of a pair, group 1 the second, all four
+    // units) and, when their count is odd, a last tile split two units per
+    // group.  Each keeps the units whose first key is at or below the wave's
+    // last query (n1: group 0's light units). ----
     const int qwL = qa * kBQ + wq * 32, qwH = qb * kBQ + wq * 32;
     const int n1 = grp == 0 ? (Tl > 0 ? min(4 * Tl, (qwL + 31) / 32 + 1) : 0) : 4 * Tl;
-    int n2 = 0;
-    for (int t = Tl; t < Th; t++)
-        for (int e = 0; e < 2; e++)
-            n2 += (t * kPKV + (2 * grp + e) * 32 <= qwH + 31) ? 1 : 0;
-    const int ntot = n1 + n2;
 
     float c = p.scale * 1.4426950408889634f;  // log2 units
     const bool neg = c < 0.0f;
@@ -779,71 +776,112 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
     fetch(2, raw);
     __syncthreads();
 
-    int k = 0;          // next unit of this wave
-    bool have = false;  // sA holds S^T of unit k
+    // ---- main loop.  Invariant at the start of a step at tile t: tiles t and
+    // t + 1 are staged in ring slots t % 4, (t + 1) % 4 and visible, and `raw`
+    // holds tile t + 2.  A single step (segment 1, or a last odd tile of
+    // segment 2) stages t + 2, fetches t + 3 and takes tile t: group 0 the light
+    // queries (then the heavy ones), group 1 the heavy ones, four units each;
+    // on the last odd tile of segment 2 each group takes two units.  A double
+    // step (segment 2) takes tiles t and t + 1: group 0 all units of tile t,
+    // group 1 all units of tile t + 1 (heavy queries), and stages t + 2 and
+    // t + 3, so a barrier serves eight units per wave instead of four.  Every
+    // slot written held a tile finished before an earlier barrier.  The
+    // look-ahead S MFMAs go into the next tile where that tile is already
+    // visible: not across a double step's end, nor for group 1 into segment 2. ----
+    int k = 0;          // light units done (group 0, segment 1)
+    bool have = false;  // sA holds S^T of this wave's next unit
     f16v_t sA, sB;
-    // units of this wave in tile t, and the first of them
-    auto count_in = [&](int t) {
-        return t < Tl ? min(max(n1 - 4 * t, 0), 4) : min(max(n2 - 2 * (t - Tl), 0), 2);
-    };
-    auto first_h = [&](int t) { return t < Tl ? 0 : 2 * grp; };
-
-    int slot = 0;  // ring slot of tile t
-    for (int t = 0; t < Th; t++) {
-        {
-            const int nslot = slot == NBUF - 1 ? 0 : slot + 1;
-            const int sslot = nslot == NBUF - 1 ? 0 : nslot + 1;  // tile t + 2
-            if (t + 2 < Th) {  // raw holds tile t + 2 (fetched one tile ago)
-                stage(raw, sslot);
-                fetch(t + 3, raw);
-            }
-            const int cnt = count_in(t);
-            const int h0 = first_h(t);
-            const int key_t = t * kPKV;
-            // look-ahead of the tile's last unit: the first unit of tile t + 1,
-            // when this wave has one and it uses the same queries
-            const bool set_ends = light && k + cnt == n1;
-            const bool next_ok = !set_ends && t + 1 < Th && count_in(t + 1) > 0;
-            const int h_next = next_ok ? first_h(t + 1) : h0;
-            const int s_next = next_ok ? nslot : slot;
-            const bool full = cnt == (t < Tl ? 4 : 2);
-            const bool unmasked = key_t + kPKV - 1 <= qw && key_t + kPKV <= M;
-            if (full && unmasked) {
-                // fast path: straight-line units, scores ping-ponging between sA and sB
-                if (!have) scores_now(slot, h0, sA);
-                unit_core(slot, h0, 0, false, sA, slot, h0 + 1, sB);
-                if (cnt == 4) {
-                    unit_core(slot, h0 + 1, 0, false, sB, slot, h0 + 2, sA);
-                    unit_core(slot, h0 + 2, 0, false, sA, slot, h0 + 3, sB);
-                    unit_core(slot, h0 + 3, 0, false, sB, s_next, h_next, sA);
-                } else {
-                    unit_core(slot, h0 + 1, 0, false, sB, s_next, h_next, sA);
-                }
-                k += cnt;
-                have = next_ok;
-                if (set_ends) switch_to_heavy();
-            } else {
-                // general path: up to four units, each with the mask where needed
+    // units u0 .. u0 + nu - 1 of tile t whose first key is at or below the wave's heavy queries
+    auto units_heavy = [&](int t, int u0, int nu) {
+        int n = 0;
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    if (u < cnt) {
-                        const int hh = h0 + u;
-                        if (!have) scores_now(slot, hh, sA);
-                        const bool last = u + 1 == cnt;
-                        const int nsl = last ? s_next : slot;
-                        const int hn = last ? h_next : hh + 1;
-                        const int key0 = key_t + hh * 32;
-                        unit_core(slot, hh, key0, key0 + 31 > qw || key0 + 31 >= M, sA, nsl, hn, sB);
-                        sA = sB;
-                        have = !last || next_ok;
-                    }
-                }
-                k += cnt;
-                if (set_ends) switch_to_heavy();
+        for (int u = 0; u < 4; u++) n += (u >= u0 && u < u0 + nu && t * kPKV + u * 32 <= qwH + 31) ? 1 : 0;
+        return n;
+    };
+    const int Tdbl = Tl + ((Th - Tl) & ~1);  // double steps over [Tl, Tdbl); a single split step at Tdbl if odd
+    // this wave's units in single-step tile t, and the first of them
+    auto count_single = [&](int t) {
+        if (t < Tl) return grp == 0 ? min(max(n1 - 4 * t, 0), 4) : units_heavy(t, 0, 4);
+        return units_heavy(t, 2 * grp, 2);
+    };
+    auto first_single = [&](int t) { return t < Tl ? 0 : 2 * grp; };
+
+    // cnt units of tile t (ring slot `slot`) from unit h0, S^T of the first in
+    // sA when `have`; the last unit's look-ahead goes to (s_next, h_next) when next_ok
+    auto run_tile = [&](int t, int slot, int cnt, int h0, bool next_ok, int s_next, int h_next) {
+        if (cnt == 0) return;
+        const int key_t = t * kPKV;
+        const bool full = cnt == ((t >= Tdbl && t >= Tl) ? 2 : 4);
+        const bool unmasked = key_t + kPKV - 1 <= qw && key_t + kPKV <= M;
+        if (full && unmasked) {
+            // fast path: straight-line units, scores ping-ponging between sA and sB
+            if (!have) scores_now(slot, h0, sA);
+            const int sn = next_ok ? s_next : slot, hn = next_ok ? h_next : h0;
+            if (cnt == 4) {
+                unit_core(slot, h0, 0, false, sA, slot, h0 + 1, sB);
+                unit_core(slot, h0 + 1, 0, false, sB, slot, h0 + 2, sA);
+                unit_core(slot, h0 + 2, 0, false, sA, slot, h0 + 3, sB);
+                unit_core(slot, h0 + 3, 0, false, sB, sn, hn, sA);
+            } else {
+                unit_core(slot, h0, 0, false, sA, slot, h0 + 1, sB);
+                unit_core(slot, h0 + 1, 0, false, sB, sn, hn, sA);
             }
-            __syncthreads();
-            slot = nslot;
+            have = next_ok;
+        } else {
+            // general path: up to four units, each with the mask where needed
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (u < cnt) {
+                    const int hh = h0 + u;
+                    if (!have) scores_now(slot, hh, sA);
+                    const bool last = u + 1 == cnt;
+                    const int nsl = last ? (next_ok ? s_next : slot) : slot;
+                    const int hn = last ? (next_ok ? h_next : hh) : hh + 1;
+                    const int key0 = key_t + hh * 32;
+                    unit_core(slot, hh, key0, key0 + 31 > qw || key0 + 31 >= M, sA, nsl, hn, sB);
+                    sA = sB;
+                    have = !last || next_ok;
+                }
+            }
         }
+    };
+
+    int t = 0;
+    while (t < Th) {
+        const bool dbl = t >= Tl && t < Tdbl;
+        if (t + 2 < Th) stage(raw, (t + 2) & 3);
+        if (t + 3 < Th) fetch(t + 3, raw);  // double step: staged at its end
+        int mt = t, cnt, h0 = 0, h_next = 0;
+        bool next_ok = false, set_ends = false;
+        if (!dbl) {
+            cnt = count_single(t);
+            h0 = first_single(t);
+            // look-ahead of the tile's last unit: this wave's first unit of the
+            // next step, when that step starts it at tile t + 1 (visible) with the
+            // same queries
+            set_ends = light && k + cnt == n1;
+            if (!set_ends && t + 1 < Th) {
+                if (t + 1 < Tl || t + 1 >= Tdbl) {
+                    next_ok = count_single(t + 1) > 0;
+                    h_next = first_single(t + 1);
+                } else if (grp == 0) {  // next: a double step, whose first tile is group 0's
+                    next_ok = units_heavy(t + 1, 0, 4) > 0;
+                }
+            }
+        } else {
+            mt = t + grp;  // this group's tile of the pair
+            cnt = units_heavy(mt, 0, 4);
+        }
+        run_tile(mt, mt & 3, cnt, h0, next_ok, (t + 1) & 3, h_next);
+        if (!dbl) {
+            if (t < Tl && grp == 0) k += cnt;
+            if (set_ends) switch_to_heavy();
+        } else {
+            if (t + 3 < Th) stage(raw, (t + 3) & 3);
+            if (t + 4 < Th) fetch(t + 4, raw);
+        }
+        __syncthreads();
+        t += dbl ? 2 : 1;
     }
 
     // ---- merge group 0's partial state for the heavy queries into group 1's ----
@@ -875,7 +913,7 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
         store(l > 0.0f ? 1.0f / l : 0.0f);
     }
 }
-constexpr size_t kPipeLds = 3 * (size_t)(kPKV * (64 + 8) + 64 * (kPKV + kPVPad)) * 2;
+constexpr size_t kPipeLds = 4 * (size_t)(kPKV * (64 + 8) + 64 * (kPKV + kPVPad)) * 2;
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
     dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
