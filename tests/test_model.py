@@ -119,6 +119,17 @@ def test_model_batch_of_one_and_no_cache(bridge):
                              intermediate_dim=256, vocab_size=256)
     m = model.TransformerModel(cfg)
     m.init_synthetic_weights(seed=5)
+    # the reference's seeds and draw order (src/engine/model.py:307-334)
+    emb = (np.random.RandomState(5).randn(256, 256) * 0.02).astype(np.float16)
+    np.testing.assert_array_equal(_host(m.embedding.weight), emb)
+    scale = 0.5 / np.sqrt(256)
+    import modules
+    np.testing.assert_array_equal(
+        _host(m.lm_head.weight),
+        _host(modules.generate_synthetic_quantized_weights(0, 256, 256, scale=scale, seed=5 + 9999)))
+    np.testing.assert_array_equal(
+        _host(m.layers[0].w_up.weight),
+        _host(modules.generate_synthetic_quantized_weights(0, 256, 256, scale=scale, seed=5 + 100 + 5 * 7)))
     a = m([[1, 2, 3, 4, 5]], use_cache=False)
     assert a.shape == (1, 5, 256) and m.layers[0].kv_q8 is None
     b = m([1, 2, 3, 4, 5])
