@@ -225,7 +225,8 @@ M4_API int m4_bridge_dispatch_gemm_noalloc(void* X_ptr, size_t X_bytes, void* W_
 M4_API int m4_bridge_set_stream(void* stream);
 /* The hipStream_t work is issued on. */
 M4_API void* m4_bridge_get_stream(void);
-/* Text of the last device error seen by the bridge ("" if none). */
+/* Text of the last error this thread's bridge calls saw ("" if none); per
+ * thread, like errno, so a caller reads the message of its own failed call. */
 M4_API const char* m4_bridge_last_error(void);
 
 /* ---- roofline probes (quant_router_kernels.metal:71-104, timed as in

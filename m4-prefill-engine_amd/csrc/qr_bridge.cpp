@@ -34,7 +34,7 @@ bool g_initialized = false;
 int g_device = 0;
 hipStream_t g_own_stream = nullptr;
 hipStream_t g_stream = nullptr;
-std::string g_last_error;
+thread_local std::string g_last_error;  // per thread, like errno: a caller reads the message of its own failed call
 
 struct Staged {
     void* dev;
@@ -873,6 +873,7 @@ double m4_bridge_get_uma_footprint_mb(void) {
         fclose(f);
     }
     double host_mb = (double)rss * 4096.0 / (1024.0 * 1024.0);
+    std::lock_guard<std::mutex> lk(g_mu);  // the byte counts change under concurrent dispatches
     return host_mb + (double)(g_ws_bytes + g_attn_ws_bytes + g_staged_bytes + g_pool_bytes + g_sk_ws_floats * 4 +
                               g_retired_bytes) /
                          (1024.0 * 1024.0);
@@ -915,7 +916,10 @@ int m4_bridge_set_stream(void* stream) {
     return 0;
 }
 
-void* m4_bridge_get_stream(void) { return g_stream; }
+void* m4_bridge_get_stream(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_stream;
+}
 
 const char* m4_bridge_last_error(void) { return g_last_error.c_str(); }
 
