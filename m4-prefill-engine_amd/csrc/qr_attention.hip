@@ -85,8 +85,11 @@ hipError_t launch_quantize_q8_0(const _Float16* src, uint8_t* dst, size_t nblock
 // --------------------------------------------------------------------------
 // Flash attention
 // --------------------------------------------------------------------------
-constexpr int kBQ = 128;      // queries per workgroup
-constexpr int kBKV = 64;      // keys per tile
+constexpr int kBQ = 128;      // queries per query tile
+constexpr int kBKV = 64;      // keys per tile of the cache pass; the fp16 cache pads M to a multiple
+// The attention kernel reads a dequantized fp16 working copy of the cache: K'
+// [H, Mp, D] (row-major) and V'^T [H, D, Mp] (keys contiguous per dim), Mp = M
+// rounded up to whole 64-key tiles, so its LDS tiles are plain 16-byte copies.
 
 // Two Q8_0 codes of bytes 0, 1 (HI = false) or 2, 3 (HI = true) of a code word
 // times d: the code plus 128 becomes the binary16 1024 + 128 + q through the
@@ -97,40 +100,6 @@ __device__ __forceinline__ uint32_t q8_pair(uint32_t codes, h2_t d) {
     const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
     const uint32_t u = codes ^ 0x80808080u;  // two's complement byte -> q + 128
     return as_u32((as_h2(HI ? nib_pair_hi(u) : nib_pair_lo(u)) - off) * d);
-}
-
-// Staging from a dequantized fp16 cache: K' [H, Mp, D] (row-major) and V'^T
-// [H, D, Mp] (keys contiguous per dim), Mp = M rounded up to whole 64-key
-// tiles.  Both LDS tiles are then plain 16-byte copies: no per-tile decode.
-template <int D>
-struct AttnRawF16 {
-    static constexpr int CH = D / 32;  // 16-byte chunks per thread for each of K and V^T
-    u4_t k[CH];
-    u4_t v[CH];
-};
-
-template <int D>
-__device__ __forceinline__ void attn_fetch_f16(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int k0, int Mp,
-                                               int tid, AttnRawF16<D>& raw) {
-#pragma unroll
-    for (int i = 0; i < AttnRawF16<D>::CH; i++) {
-        const int c = tid + 256 * i;
-        const int key = c / (D / 8), kc = c % (D / 8);        // K: 64 keys x D/8 chunks
-        raw.k[i] = ld_b128(kr, (uint32_t)((k0 + key) * D + kc * 8) * 2u);
-        const int d = c / 8, vc = c % 8;                        // V^T: D rows x 8 chunks of 8 keys
-        raw.v[i] = ld_b128(vr, (uint32_t)(d * Mp + k0 + vc * 8) * 2u);
-    }
-}
-
-template <int D>
-__device__ __forceinline__ void attn_stage_f16(const AttnRawF16<D>& raw, int tid, _Float16* Ks, _Float16* Vt) {
-    constexpr int KROW = D + 8, VROW = kBKV + 8;
-#pragma unroll
-    for (int i = 0; i < AttnRawF16<D>::CH; i++) {
-        const int c = tid + 256 * i;
-        *reinterpret_cast<u4_t*>(Ks + (c / (D / 8)) * KROW + (c % (D / 8)) * 8) = raw.k[i];
-        *reinterpret_cast<u4_t*>(Vt + (c / 8) * VROW + (c % 8) * 8) = raw.v[i];
-    }
 }
 
 // Dequantized fp16 cache for the attention kernel, one workgroup per 64-key
@@ -276,267 +245,55 @@ __global__ void __launch_bounds__(256) kv_prep_kernel(const void* Ksrc, const vo
     }
 }
 
-// Flash attention over a Q8_0 K/V cache (one workgroup = 4 wave64s = 128
-// queries of one head).
-//  * Each wave owns 32 queries and computes S^T = K . Q^T with
-//    v_mfma_f32_32x32x16_f16, so a lane owns ONE query column: softmax row
-//    statistics are lane-local over its accumulator rows plus one exchange
-//    with the partner lane (l ^ 32).
-//  * K/V tiles of 64 keys are dequantized once per workgroup from Q8_0 into a
-//    double-buffered LDS stage (K as [key][d], V transposed as [d][key]); the
-//    raw blocks of tile t + 1 are fetched while tile t is multiplied, and
-//    decoded after it, so one barrier per tile and no exposed fetch latency.
-//  * Softmax in log2 units with the scale folded into one fma per score; the
-//    causal mask is applied only on tiles that cross the wave's diagonal; the
-//    running output is rescaled only when some lane's maximum moved.
-//  * P stays in registers: the S^T accumulator of a lane already holds the
-//    8 keys that lane supplies as the B operand of O^T = V^T . P^T.
-//  * fp32 running max / sum / output accumulators (the reference keeps S, P
-//    and O in half); the output is rounded to fp16 once.
-template <int D>
-__global__ void __launch_bounds__(256, D <= 64 ? 2 : 1) flash_attn_q8_0_kernel(AttnParams p) {
-    constexpr int KROW = D + 8;                // LDS row (halfs) of K tile [key][d]
-    constexpr int VROW = kBKV + 8;             // LDS row (halfs) of V^T tile [d][key]
-    constexpr int DT = D / 32;                 // 32-row output tiles along d
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kBKV * KROW];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VROW];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 5, j = lane & 31;
-    const int M = (int)p.M;
-    const int qtiles = (M + kBQ - 1) / kBQ;
-    // Work of a query tile grows with its index (causal).  Rank r orders the
-    // (tile, head) pairs heaviest first; workgroup b of the first half takes
-    // rank b and workgroup b + half rank total - 1 - b, so the two workgroups a
-    // CU receives in dispatch order sum to about the same work everywhere.
-    const int total = qtiles * (int)p.H, half = (total + 1) / 2;
-    const int b = (int)blockIdx.x;
-    const int rank = b < half ? b : total - 1 - (b - half);
-    const int qt = qtiles - 1 - rank / (int)p.H;
-    const int h = rank % (int)p.H;
-    const int q0 = qt * kBQ;
-    const int qw = q0 + wave * 32;                 // this wave's first query
-    const int my_q = qw + j;                       // this lane's query
-
-    const size_t head_elems = (size_t)M * D;
-    const _Float16* Qh = p.Q + (size_t)h * head_elems;
-    const int hk = p.Hkv ? h / ((int)p.H / (int)p.Hkv) : h;  // grouped-query: shared KV head
-    const int Mp = (int)p.Mp;
-    const uint32_t bytes = (uint32_t)((size_t)Mp * D * 2);
-    auto kr = make_rsrc(p.Kf + (size_t)hk * Mp * D, bytes);
-    auto vr = make_rsrc(p.Vtf + (size_t)hk * Mp * D, bytes);
-    using Raw = AttnRawF16<D>;
-    auto fetch = [&](int k0, Raw& raw) { attn_fetch_f16<D>(kr, vr, k0, Mp, tid, raw); };
-    auto stage = [&](const Raw& raw, int k0, _Float16* Kd, _Float16* Vd) { attn_stage_f16<D>(raw, tid, Kd, Vd); };
-
-    const int q_last = min(q0 + kBQ, M) - 1;
-    const int ntiles = q_last / kBKV + 1;
-
-    // ---- prologue: tile 0 staged, tile 1 in flight ----
-    Raw rawA, rawB;
-    fetch(0, rawA);
-    if (ntiles > 1) fetch(kBKV, rawB);
-
-    // Q^T fragments (B operand): lane holds Q[my_q][kk*16 + 8g .. +7].
-    h8_t qf[D / 16];
-    {
-        auto qr_ = make_rsrc(Qh, (uint32_t)(head_elems * 2));
-#pragma unroll
-        for (int kk = 0; kk < D / 16; kk++) {
-            uint32_t off = my_q < M ? ((uint32_t)my_q * D + kk * 16 + 8 * g) * 2u : kOOB;
-            u4_t v = ld_b128(qr_, off);
-            qf[kk] = __builtin_bit_cast(h8_t, v);
-        }
-    }
-    stage(rawA, 0, Ks[0], Vt[0]);
-    __syncthreads();
-
-    // scores -> log2 units: s * c with c > 0 (a negative scale flips the sign
-    // of Q once, exactly, so the running maximum stays a maximum of s)
-    float c = p.scale * 1.4426950408889634f;
-    if (c < 0.0f) {
-        c = -c;
-#pragma unroll
-        for (int kk = 0; kk < D / 16; kk++) qf[kk] = -qf[kk];
-    }
-    float m_run = -INFINITY;
-    // o[DT] row 0 accumulates the softmax denominator: the P.V MFMAs also
-    // multiply P by a constant A operand whose row 0 is all ones (lanes of
-    // row j = 0), so the row sums ride on the matrix pipe instead of VALU adds
-    // and use the same fp16 P as the numerator.
-    f16v_t o[DT + 1];
-#pragma unroll
-    for (int t = 0; t <= DT; t++) o[t] = f16v_t{};
-    const _Float16 one = j == 0 ? (_Float16)1.0f : (_Float16)0.0f;
-    const h8_t ones = {one, one, one, one, one, one, one, one};
-
-    auto compute = [&](int kt) {
-        const int k0 = kt * kBKV;
-        if (k0 > qw + 31) return;  // whole tile above this wave's diagonal
-        const _Float16* Kb = Ks[kt & 1];
-        const _Float16* Vb = Vt[kt & 1];
-        // ---- S^T = K . Q^T : two 32-key tiles; all K fragments read first ----
-        h8_t ka[2][D / 16];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int kk = 0; kk < D / 16; kk++)
-                ka[ks][kk] = *reinterpret_cast<const h8_t*>(Kb + (ks * 32 + j) * KROW + kk * 16 + 8 * g);
-        f16v_t s[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            s[ks] = f16v_t{};
-#pragma unroll
-            for (int kk = 0; kk < D / 16; kk++)
-                s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks][kk], qf[kk], s[ks], 0, 0, 0);
-        }
-        // V^T fragments of the P.V step, read now so their latency hides under
-        // the softmax: step (ks, t2) needs keys 32ks + 16t2 + 4g + {0..3, 8..11}
-        u4_t va[2][2][DT];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-                for (int t = 0; t < DT; t++) {
-                    const _Float16* row = Vb + (t * 32 + j) * VROW + ks * 32 + t2 * 16 + 4 * g;
-                    const u2_t lo = *reinterpret_cast<const u2_t*>(row);
-                    const u2_t hi = *reinterpret_cast<const u2_t*>(row + 8);
-                    va[ks][t2][t] = u4_t{lo.x, lo.y, hi.x, hi.y};
-                }
-        // ---- causal mask (diagonal tiles only), running max ----
-        if (k0 + kBKV - 1 > qw) {
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = k0 + ks * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    s[ks][r] = (key <= my_q && key < M) ? s[ks][r] : -INFINITY;
-                }
-        }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s[ks][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        // Lazy running maximum: the reference point moves only when some lane's
-        // tile maximum exceeds it by more than 2^8 (P <= 256 in the meantime,
-        // well inside fp16 and fp32); the output rescale is skipped otherwise.
-        const float m_cand = tmax * c;
-        float alpha = 1.0f;
-        if (__any(m_cand > m_run + 8.0f)) {  // always taken on the first tile (m_run = -inf)
-            const float m_new = fmaxf(m_run, m_cand);
-            alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
-            m_run = m_new;
-        }
-        const float m_new = m_run;
-        uint32_t pk[2][8];  // P as half2 words in accumulator order (one RNE pair conversion)
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][r], c, -m_new));
-                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks][r + 1], c, -m_new));
-                const f2_t e = {e0, e1};
-                pk[ks][r >> 1] = as_u32(__builtin_convertvector(e, h2_t));
-            }
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int t = 0; t < DT; t++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[t][r] *= alpha;
-            o[DT][0] *= alpha;  // the only nonzero row of the denominator tile
-        }
-
-        // ---- O^T += V^T . P^T : 4 k16 steps over the 64 keys ----
-        // step (ks, t2): B operand = P rows r = 8*t2 .. 8*t2+7 of tile ks, i.e. keys
-        // 32ks + 16t2 + 4g + {0..3} and 32ks + 16t2 + 8 + 4g + {0..3}.
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int t2 = 0; t2 < 2; t2++) {
-                u4_t bw = {pk[ks][4 * t2], pk[ks][4 * t2 + 1], pk[ks][4 * t2 + 2], pk[ks][4 * t2 + 3]};
-                h8_t b = __builtin_bit_cast(h8_t, bw);
-#pragma unroll
-                for (int t = 0; t < DT; t++)
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[ks][t2][t]), b, o[t], 0,
-                                                                  0, 0);
-                o[DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, b, o[DT], 0, 0, 0);
-            }
-    };
-
-    // ---- main loop, unrolled by two for the raw register sets:
-    // iteration kt: fetch tile kt + 2, multiply tile kt, stage tile kt + 1 ----
-    for (int kt = 0; kt < ntiles; kt += 2) {
-        if (kt + 2 < ntiles) fetch((kt + 2) * kBKV, rawA);
-        compute(kt);
-        if (kt + 1 < ntiles) stage(rawB, (kt + 1) * kBKV, Ks[(kt + 1) & 1], Vt[(kt + 1) & 1]);
-        __syncthreads();
-        if (kt + 1 >= ntiles) break;
-        if (kt + 3 < ntiles) fetch((kt + 3) * kBKV, rawB);
-        compute(kt + 1);
-        if (kt + 2 < ntiles) stage(rawA, (kt + 2) * kBKV, Ks[kt & 1], Vt[kt & 1]);
-        __syncthreads();
-    }
-
-    // ---- normalize and store ----
-    // denominator of query j: row 0 of the ones tile, held by lane j (lanes 32..63 hold rows 4..7)
-    const float l_tot = __shfl(o[DT][0], j, 64);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (my_q < M) {
-#pragma unroll
-        for (int t = 0; t < DT; t++)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const int d0 = t * 32 + 8 * r4 + 4 * g;
-                uint32_t w0 = pack_h2(f2h_bits(o[t][4 * r4] * inv), f2h_bits(o[t][4 * r4 + 1] * inv));
-                uint32_t w1 = pack_h2(f2h_bits(o[t][4 * r4 + 2] * inv), f2h_bits(o[t][4 * r4 + 3] * inv));
-                size_t idx = p.o_token_major ? ((size_t)my_q * p.H + h) * D + d0 : (size_t)h * head_elems + (size_t)my_q * D + d0;
-                *reinterpret_cast<u2_t*>(p.O + idx) = u2_t{w0, w1};
-            }
-    }
-}
-
 // --------------------------------------------------------------------------
-// Software-pipelined causal attention over the fp16 cache (D = 64), with the
-// query-tile pairing that balances the causal work: one workgroup of 8 waves per
-// (light, heavy) pair of 128-query tiles -- a and qtiles - 1 - a -- so every
-// workgroup carries the same work.  Key tiles are 128 keys (one barrier per
-// 128 keys); a tile is four 32-key units.  Group 0 takes the light tile's
-// queries and group 1 the heavy tile's on the key tiles both need; on the
-// heavy tile's remaining key tiles group 0 takes units 0-1 and group 1 units
-// 2-3 of each tile for the heavy queries, and group 0's partial softmax state
-// is merged into group 1's at the end.  Units whose keys all lie above a
-// wave's diagonal are skipped.
+// Software-pipelined causal attention over the fp16 cache, with the
+// query-tile pairing that balances the causal work: one workgroup per (light,
+// heavy) pair of 128-query tiles -- a and qtiles - 1 - a -- so every
+// workgroup carries the same work.  A key tile is 32-key units (four at D =
+// 64, two at D = 128); units whose keys all lie above a wave's diagonal are
+// skipped.
+//
+// D = 64 (NG = 2, 8 waves, two per SIMD): group 0 takes the light tile's
+// queries and group 1 the heavy tile's on the key tiles both need; the heavy
+// tile's remaining key tiles go in pairs, one tile of a pair per group (a last
+// odd tile split two units per group), and group 0's partial softmax state is
+// merged into group 1's at the end.
+// D = 128 (NG = 1, 4 waves, one per SIMD, so a wave has the registers for the
+// 32 x 128 output tile and both fragment sets): the light tile's key tiles,
+// then the heavy tile's, as one stream, two tiles per barrier.
 //
 // Pipelining: while the softmax of unit u runs on the VALU, the S^T = K . Q^T
 // MFMAs of unit u + 1 and the O^T += V^T . P^T MFMAs of unit u are issued from
 // the same fenced instruction sequence, so the matrix pipe and the vector ALU
-// work side by side inside every wave.  K/V tiles sit in a 3-deep LDS ring
-// (tile t read, tile t + 1 read by the look-ahead S, tile t + 2 being
-// written).  Arithmetic per unit: log2-unit softmax with the scale folded into
-// one fma, a lazily moved reference point (threshold 2^8, decided per lane
-// half, the halves combined only when it moves), fp32 state, P rounded to
-// fp16 for the MFMA and for the row sums.
+// work side by side inside every wave.  K/V tiles sit in a 4-deep LDS ring
+// (tiles t and t + 1 read, the look-ahead S reading ahead where that tile is
+// already visible, tiles t + 2 and t + 3 being written).  Arithmetic per
+// unit: log2-unit softmax with the scale folded into one fma, a lazily moved
+// reference point (threshold 2^8, decided per lane half, the halves combined
+// only when it moves), fp32 state, P rounded to fp16 for the MFMA and for the
+// row sums.
 // --------------------------------------------------------------------------
-constexpr int kPKV = 128;  // keys per tile of the pipelined kernel
+// keys per tile of the pipelined kernel: 128 at D = 64, 64 at D = 128 (the
+// 4-deep ring of K and V^T tiles then fits the LDS at either width)
+constexpr int pipe_keys(int D) { return D == 64 ? 128 : 64; }
 constexpr int kPVPad = 4;  // halfs of padding per V^T row of its LDS tiles
 
-template <int D>
-__global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
-    static_assert(D == 64, "chunk schedule and per-thread staging written for D = 64");
-    // V^T rows of 132 halfs (66 dwords): the fragment reads of lanes j and
-    // j + 16 land 32 banks apart (a 68-dword row put them on the same banks)
+template <int D, int NG>  // NG: wave groups of 4 (2: the pair schedule; 1: the two tiles one after the other)
+__global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p) {
+    static_assert(D == 64 || D == 128, "chunk schedules written for D = 64 and D = 128");
+    constexpr int kPKV = pipe_keys(D), UPT = kPKV / 32;  // units (32 keys) per tile
+    // V^T rows of kPKV + 4 halfs (66 or 34 dwords): the fragment reads of
+    // lanes j and j + 16 land 32 banks apart (a 68-dword row put them on the
+    // same banks)
     constexpr int KROW = D + 8, VROW = kPKV + kPVPad, DT = D / 32;
-    constexpr int NT = 512;
+    constexpr int NT = 256 * NG;
     constexpr int KT = kPKV * KROW, VT = D * VROW, TILE = KT + VT;
     constexpr int NBUF = 4;
     constexpr int KCH = kPKV * (D / 8) / NT, VCH = D * (kPKV / 8) / NT;  // 16-byte chunks per thread
     extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave >> 2, wq = wave & 3;
+    const int grp = NG == 2 ? wave >> 2 : 0, wq = wave & 3;
     const int g = lane >> 5, j = lane & 31;
     const int M = (int)p.M, Mp = (int)p.Mp;
     const int qtiles = (M + kBQ - 1) / kBQ;
@@ -599,7 +356,7 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
     // group.  Each keeps the units whose first key is at or below the wave's
     // last query (n1: group 0's light units). ----
     const int qwL = qa * kBQ + wq * 32, qwH = qb * kBQ + wq * 32;
-    const int n1 = grp == 0 ? (Tl > 0 ? min(4 * Tl, (qwL + 31) / 32 + 1) : 0) : 4 * Tl;
+    const int n1 = grp == 0 ? (Tl > 0 ? min(UPT * Tl, (qwL + 31) / 32 + 1) : 0) : UPT * Tl;
 
     float c = p.scale * 1.4426950408889634f;  // log2 units
     const bool neg = c < 0.0f;
@@ -658,25 +415,31 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
             }
         }
         // V^T fragments of this unit, K fragments of the look-ahead unit
+        // (at D = 128 the second halves are read inside the chunk schedule,
+        // once the registers of the first halves are free)
         u4_t va[2][DT];
-        {
-            const _Float16* Vb = smem + slot * TILE + KT + hh * 32 + vbase;
+        const _Float16* Vb = smem + slot * TILE + KT + hh * 32 + vbase;
+        auto read_va = [&](int t2) {
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-                for (int tt = 0; tt < DT; tt++) {
-                    const _Float16* row = Vb + tt * 32 * VROW + t2 * 16;
-                    const u2_t lo = *reinterpret_cast<const u2_t*>(row);
-                    const u2_t hi = *reinterpret_cast<const u2_t*>(row + 8);
-                    va[t2][tt] = u4_t{lo.x, lo.y, hi.x, hi.y};
-                }
-        }
+            for (int tt = 0; tt < DT; tt++) {
+                const _Float16* row = Vb + tt * 32 * VROW + t2 * 16;
+                const u2_t lo = *reinterpret_cast<const u2_t*>(row);
+                const u2_t hi = *reinterpret_cast<const u2_t*>(row + 8);
+                va[t2][tt] = u4_t{lo.x, lo.y, hi.x, hi.y};
+            }
+        };
         h8_t kn_[D / 16];
-        {
-            const _Float16* Kb = smem + nsl * TILE + hn * 32 * KROW + kbase;
+        const _Float16* Kb = smem + nsl * TILE + hn * 32 * KROW + kbase;
+        auto read_kn = [&](int kk0, int kk1) {
 #pragma unroll
-            for (int kk = 0; kk < D / 16; kk++)
-                kn_[kk] = *reinterpret_cast<const h8_t*>(Kb + kk * 16);
+            for (int kk = kk0; kk < kk1; kk++) kn_[kk] = *reinterpret_cast<const h8_t*>(Kb + kk * 16);
+        };
+        read_va(0);
+        if constexpr (D == 64) {
+            read_va(1);
+            read_kn(0, D / 16);
+        } else {
+            read_kn(0, 4);
         }
         // Row maximum: each lane's half (16 keys) decides whether the shared
         // reference point must move; only then are the two halves combined.
@@ -716,34 +479,70 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
             const h8_t b = __builtin_bit_cast(h8_t, u4_t{pk[4 * t2], pk[4 * t2 + 1], pk[4 * t2 + 2], pk[4 * t2 + 3]});
             o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, va[t2][tt]), b, o[tt], 0, 0, 0);
         };
-        static_assert(DT == 2, "chunk schedule written for D = 64");
+        auto smf = [&](int kk) {  // look-ahead S^T MFMA over d = 16 kk .. 16 kk + 15
+            s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[kk], qf[kk], kk ? s_out : f16v_t{}, 0, 0, 0);
+        };
         // raised wave priority for the interleaved block: the SIMD's other
         // wave (in its row-max / fragment-read phase) yields issue slots to it
         __builtin_amdgcn_s_setprio(1);
         // each exponential is converted one chunk after it is issued, and each
         // O MFMA follows the conversions it needs by a chunk where possible
         __builtin_amdgcn_sched_barrier(0);
-        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[0], qf[0], f16v_t{}, 0, 0, 0);
-        exps(0);
-        __builtin_amdgcn_sched_barrier(0);
-        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[1], qf[1], s_out, 0, 0, 0);
-        exps(4);
-        cvts(0);
-        __builtin_amdgcn_sched_barrier(0);
-        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[2], qf[2], s_out, 0, 0, 0);
-        exps(8);
-        cvts(4);
-        __builtin_amdgcn_sched_barrier(0);
-        s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn_[3], qf[3], s_out, 0, 0, 0);
-        pv(0, 0);
-        exps(12);
-        cvts(8);
-        __builtin_amdgcn_sched_barrier(0);
-        pv(0, 1);
-        cvts(12);
-        __builtin_amdgcn_sched_barrier(0);
-        pv(1, 0);
-        pv(1, 1);
+        if constexpr (D == 64) {
+            smf(0);
+            exps(0);
+            __builtin_amdgcn_sched_barrier(0);
+            smf(1);
+            exps(4);
+            cvts(0);
+            __builtin_amdgcn_sched_barrier(0);
+            smf(2);
+            exps(8);
+            cvts(4);
+            __builtin_amdgcn_sched_barrier(0);
+            smf(3);
+            pv(0, 0);
+            exps(12);
+            cvts(8);
+            __builtin_amdgcn_sched_barrier(0);
+            pv(0, 1);
+            cvts(12);
+            __builtin_amdgcn_sched_barrier(0);
+            pv(1, 0);
+            pv(1, 1);
+        } else {  // D = 128: twice the MFMAs per unit against the same softmax
+            smf(0);
+            smf(1);
+            exps(0);
+            __builtin_amdgcn_sched_barrier(0);
+            smf(2);
+            smf(3);
+            exps(4);
+            cvts(0);
+            read_kn(4, 8);
+            __builtin_amdgcn_sched_barrier(0);
+            smf(4);
+            smf(5);
+            exps(8);
+            cvts(4);
+            __builtin_amdgcn_sched_barrier(0);
+            smf(6);
+            smf(7);
+            pv(0, 0);
+            pv(0, 1);
+            exps(12);
+            cvts(8);
+            read_va(1);
+            __builtin_amdgcn_sched_barrier(0);
+            pv(0, 2);
+            pv(0, 3);
+            cvts(12);
+            __builtin_amdgcn_sched_barrier(0);
+            pv(1, 0);
+            pv(1, 1);
+            pv(1, 2);
+            pv(1, 3);
+        }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
@@ -767,15 +566,6 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
         for (int tt = 0; tt < DT; tt++) o[tt] = f16v_t{};
     };
 
-    // ---- prologue ----
-    Raw raw;
-    fetch(0, raw);
-    stage(raw, 0);
-    fetch(1, raw);
-    stage(raw, 1);
-    fetch(2, raw);
-    __syncthreads();
-
     // ---- main loop.  Invariant at the start of a step at tile t: tiles t and
     // t + 1 are staged in ring slots t % 4, (t + 1) % 4 and visible, and `raw`
     // holds tile t + 2.  A single step (segment 1, or a last odd tile of
@@ -795,29 +585,29 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
     auto units_heavy = [&](int t, int u0, int nu) {
         int n = 0;
 #pragma unroll
-        for (int u = 0; u < 4; u++) n += (u >= u0 && u < u0 + nu && t * kPKV + u * 32 <= qwH + 31) ? 1 : 0;
+        for (int u = 0; u < UPT; u++) n += (u >= u0 && u < u0 + nu && t * kPKV + u * 32 <= qwH + 31) ? 1 : 0;
         return n;
     };
     const int Tdbl = Tl + ((Th - Tl) & ~1);  // double steps over [Tl, Tdbl); a single split step at Tdbl if odd
     // this wave's units in single-step tile t, and the first of them
     auto count_single = [&](int t) {
-        if (t < Tl) return grp == 0 ? min(max(n1 - 4 * t, 0), 4) : units_heavy(t, 0, 4);
-        return units_heavy(t, 2 * grp, 2);
+        if (t < Tl) return grp == 0 ? min(max(n1 - UPT * t, 0), UPT) : units_heavy(t, 0, UPT);
+        return units_heavy(t, grp * (UPT / 2), UPT / 2);
     };
-    auto first_single = [&](int t) { return t < Tl ? 0 : 2 * grp; };
+    auto first_single = [&](int t) { return t < Tl ? 0 : grp * (UPT / 2); };
 
     // cnt units of tile t (ring slot `slot`) from unit h0, S^T of the first in
     // sA when `have`; the last unit's look-ahead goes to (s_next, h_next) when next_ok
     auto run_tile = [&](int t, int slot, int cnt, int h0, bool next_ok, int s_next, int h_next) {
         if (cnt == 0) return;
         const int key_t = t * kPKV;
-        const bool full = cnt == ((t >= Tdbl && t >= Tl) ? 2 : 4);
+        const bool full = cnt == ((NG == 2 && t >= Tdbl && t >= Tl) ? UPT / 2 : UPT) && cnt >= 2;
         const bool unmasked = key_t + kPKV - 1 <= qw && key_t + kPKV <= M;
         if (full && unmasked) {
             // fast path: straight-line units, scores ping-ponging between sA and sB
             if (!have) scores_now(slot, h0, sA);
             const int sn = next_ok ? s_next : slot, hn = next_ok ? h_next : h0;
-            if (cnt == 4) {
+            if (UPT == 4 && cnt == 4) {
                 unit_core(slot, h0, 0, false, sA, slot, h0 + 1, sB);
                 unit_core(slot, h0 + 1, 0, false, sB, slot, h0 + 2, sA);
                 unit_core(slot, h0 + 2, 0, false, sA, slot, h0 + 3, sB);
@@ -830,7 +620,7 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
         } else {
             // general path: up to four units, each with the mask where needed
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < UPT; u++) {
                 if (u < cnt) {
                     const int hh = h0 + u;
                     if (!have) scores_now(slot, hh, sA);
@@ -846,92 +636,149 @@ __global__ void __launch_bounds__(512) flash_attn_pipe_kernel(AttnParams p) {
         }
     };
 
-    int t = 0;
-    while (t < Th) {
-        const bool dbl = t >= Tl && t < Tdbl;
-        if (t + 2 < Th) stage(raw, (t + 2) & 3);
-        if (t + 3 < Th) fetch(t + 3, raw);  // double step: staged at its end
-        int mt = t, cnt, h0 = 0, h_next = 0;
-        bool next_ok = false, set_ends = false;
-        if (!dbl) {
-            cnt = count_single(t);
-            h0 = first_single(t);
-            // look-ahead of the tile's last unit: this wave's first unit of the
-            // next step, when that step starts it at tile t + 1 (visible) with the
-            // same queries
-            set_ends = light && k + cnt == n1;
-            if (!set_ends && t + 1 < Th) {
-                if (t + 1 < Tl || t + 1 >= Tdbl) {
-                    next_ok = count_single(t + 1) > 0;
-                    h_next = first_single(t + 1);
-                } else if (grp == 0) {  // next: a double step, whose first tile is group 0's
-                    next_ok = units_heavy(t + 1, 0, 4) > 0;
-                }
-            }
-        } else {
-            mt = t + grp;  // this group's tile of the pair
-            cnt = units_heavy(mt, 0, 4);
-        }
-        run_tile(mt, mt & 3, cnt, h0, next_ok, (t + 1) & 3, h_next);
-        if (!dbl) {
-            if (t < Tl && grp == 0) k += cnt;
+    if constexpr (NG == 1) {
+        // One group: the light tile's key tiles [0, Tl), then the heavy tile's
+        // [0, Th), as one stream of Tl + Th steps through the ring (the first
+        // Tl tiles are fetched twice).  Each wave switches to the heavy
+        // queries after its last light unit and idles until step Tl.
+        const int S = Tl + Th;
+        auto tile_of = [&](int s) { return s < Tl ? s : s - Tl; };
+        auto count_at = [&](int s) {
+            return s < Tl ? min(max(n1 - UPT * s, 0), UPT) : units_heavy(s - Tl, 0, UPT);
+        };
+        Raw raw;
+        fetch(tile_of(0), raw);
+        stage(raw, 0);
+        fetch(tile_of(1), raw);
+        stage(raw, 1);
+        fetch(tile_of(2), raw);
+        __syncthreads();
+        // step s: the units of tile_of(s); la: tile s + 1 is visible (look-ahead allowed)
+        auto do_step = [&](int s, bool la) {
+            const int cnt = count_at(s);
+            const bool set_ends = light && s < Tl && k + cnt == n1;
+            const bool next_ok = la && !set_ends && s + 1 < S && count_at(s + 1) > 0;
+            run_tile(tile_of(s), s & 3, cnt, 0, next_ok, (s + 1) & 3, 0);
+            if (s < Tl) k += cnt;
             if (set_ends) switch_to_heavy();
-        } else {
-            if (t + 3 < Th) stage(raw, (t + 3) & 3);
-            if (t + 4 < Th) fetch(t + 4, raw);
+        };
+        // Invariant at the start of an iteration at s: steps s and s + 1 are
+        // staged and visible, `raw` holds s + 2.  Two steps per barrier: s + 2
+        // is staged first, s + 3 after both steps (its slot held s - 1).
+        for (int s = 0; s < S;) {
+            const bool dbl = s + 1 < S;
+            if (s + 2 < S) stage(raw, (s + 2) & 3);
+            if (s + 3 < S) fetch(tile_of(s + 3), raw);
+            do_step(s, true);
+            if (dbl) {
+                do_step(s + 1, false);
+                if (s + 3 < S) stage(raw, (s + 3) & 3);
+                if (s + 4 < S) fetch(tile_of(s + 4), raw);
+            }
+            __syncthreads();
+            s += dbl ? 2 : 1;
+        }
+        const float l = l_run + __shfl_xor(l_run, 32);
+        store(l > 0.0f ? 1.0f / l : 0.0f);
+    } else {
+        // ---- prologue ----
+        Raw raw;
+        fetch(0, raw);
+        stage(raw, 0);
+        fetch(1, raw);
+        stage(raw, 1);
+        fetch(2, raw);
+        __syncthreads();
+
+        int t = 0;
+        while (t < Th) {
+            const bool dbl = t >= Tl && t < Tdbl;
+            if (t + 2 < Th) stage(raw, (t + 2) & 3);
+            if (t + 3 < Th) fetch(t + 3, raw);  // double step: staged at its end
+            int mt = t, cnt, h0 = 0, h_next = 0;
+            bool next_ok = false, set_ends = false;
+            if (!dbl) {
+                cnt = count_single(t);
+                h0 = first_single(t);
+                // look-ahead of the tile's last unit: this wave's first unit of the
+                // next step, when that step starts it at tile t + 1 (visible) with the
+                // same queries
+                set_ends = light && k + cnt == n1;
+                if (!set_ends && t + 1 < Th) {
+                    if (t + 1 < Tl || t + 1 >= Tdbl) {
+                        next_ok = count_single(t + 1) > 0;
+                        h_next = first_single(t + 1);
+                    } else if (grp == 0) {  // next: a double step, whose first tile is group 0's
+                        next_ok = units_heavy(t + 1, 0, UPT) > 0;
+                    }
+                }
+            } else {
+                mt = t + grp;  // this group's tile of the pair
+                cnt = units_heavy(mt, 0, UPT);
+            }
+            run_tile(mt, mt & 3, cnt, h0, next_ok, (t + 1) & 3, h_next);
+            if (!dbl) {
+                if (t < Tl && grp == 0) k += cnt;
+                if (set_ends) switch_to_heavy();
+            } else {
+                if (t + 3 < Th) stage(raw, (t + 3) & 3);
+                if (t + 4 < Th) fetch(t + 4, raw);
+            }
+            __syncthreads();
+            t += dbl ? 2 : 1;
+        }
+
+        // ---- merge group 0's partial state for the heavy queries into group 1's ----
+        constexpr int SW = DT * 16 + 2;
+        float* X = reinterpret_cast<float*>(smem);
+        static_assert(4 * 64 * SW * 4 <= NBUF * TILE * 2, "merge buffer fits the tile ring");
+        if (grp == 0) {
+            float* x = X + (wq * 64 + lane);
+    #pragma unroll
+            for (int t = 0; t < DT; t++)
+    #pragma unroll
+                for (int r = 0; r < 16; r++) x[(t * 16 + r) * 256] = o[t][r];
+            x[(DT * 16) * 256] = l_run;
+            x[(DT * 16 + 1) * 256] = m_run;
         }
         __syncthreads();
-        t += dbl ? 2 : 1;
-    }
-
-    // ---- merge group 0's partial state for the heavy queries into group 1's ----
-    constexpr int SW = DT * 16 + 2;
-    float* X = reinterpret_cast<float*>(smem);
-    static_assert(4 * 64 * SW * 4 <= NBUF * TILE * 2, "merge buffer fits the tile ring");
-    if (grp == 0) {
-        float* x = X + (wq * 64 + lane);
-#pragma unroll
-        for (int t = 0; t < DT; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) x[(t * 16 + r) * 256] = o[t][r];
-        x[(DT * 16) * 256] = l_run;
-        x[(DT * 16 + 1) * 256] = m_run;
-    }
-    __syncthreads();
-    if (grp == 1) {
-        const float* x = X + (wq * 64 + lane);
-        const float ma = x[(DT * 16 + 1) * 256];
-        const float m = fmaxf(ma, m_run);
-        const float fa = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - m);
-        const float fb = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
-#pragma unroll
-        for (int t = 0; t < DT; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[t][r] = o[t][r] * fb + x[(t * 16 + r) * 256] * fa;
-        const float lh = l_run * fb + x[(DT * 16) * 256] * fa;
-        const float l = lh + __shfl_xor(lh, 32);
-        store(l > 0.0f ? 1.0f / l : 0.0f);
+        if (grp == 1) {
+            const float* x = X + (wq * 64 + lane);
+            const float ma = x[(DT * 16 + 1) * 256];
+            const float m = fmaxf(ma, m_run);
+            const float fa = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - m);
+            const float fb = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+    #pragma unroll
+            for (int t = 0; t < DT; t++)
+    #pragma unroll
+                for (int r = 0; r < 16; r++) o[t][r] = o[t][r] * fb + x[(t * 16 + r) * 256] * fa;
+            const float lh = l_run * fb + x[(DT * 16) * 256] * fa;
+            const float l = lh + __shfl_xor(lh, 32);
+            store(l > 0.0f ? 1.0f / l : 0.0f);
+        }
     }
 }
-constexpr size_t kPipeLds = 4 * (size_t)(kPKV * (64 + 8) + 64 * (kPKV + kPVPad)) * 2;
+// LDS of the pipelined kernel: the 4-deep ring of K [key][D + 8] and V^T [D][key + 4] tiles
+constexpr size_t pipe_lds(int D) { return 4 * (size_t)(pipe_keys(D) * (D + 8) + D * (pipe_keys(D) + kPVPad)) * 2; }
+
+template <int D, int NG>
+static hipError_t launch_pipe(const AttnParams& p, hipStream_t st) {
+    const uint32_t qtiles = (p.M + kBQ - 1) / kBQ;  // a workgroup takes a light and a heavy query tile
+    static size_t attr[kMaxDevices] = {};  // the tile ring needs more than the default 64 KB of LDS
+    const hipError_t e = lds_limit_once((const void*)flash_attn_pipe_kernel<D, NG>, pipe_lds(D), attr);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((flash_attn_pipe_kernel<D, NG>), dim3(((qtiles + 1) / 2) * p.H), dim3(256 * NG), pipe_lds(D), st, p);
+    return hipGetLastError();
+}
 
 hipError_t launch_flash_attn_q8_0(const AttnParams& p, hipStream_t st) {
-    dim3 grid(((p.M + kBQ - 1) / kBQ) * p.H);
     // the kernels read the dequantized fp16 cache (launch_kv_prep)
     if (p.Kf == nullptr || p.Vtf == nullptr || p.Mp < p.M || p.Mp % kBKV) return hipErrorInvalidValue;
-    if (p.D == 64) {
-        const uint32_t qtiles = (p.M + kBQ - 1) / kBQ;
-        static size_t attr[kMaxDevices] = {};  // the 3-tile ring needs more than the default 64 KB of LDS
-        const hipError_t e = lds_limit_once((const void*)flash_attn_pipe_kernel<64>, kPipeLds, attr);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((flash_attn_pipe_kernel<64>), dim3(((qtiles + 1) / 2) * p.H), dim3(512), kPipeLds, st, p);
-        return hipGetLastError();
-    }
     switch (p.D) {
-        case 128: hipLaunchKernelGGL((flash_attn_q8_0_kernel<128>), grid, dim3(256), 0, st, p); break;
+        case 64: return launch_pipe<64, 2>(p, st);
+        case 128: return launch_pipe<128, 1>(p, st);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 uint32_t kv_padded_len(uint32_t M) { return (M + kBKV - 1) / kBKV * kBKV; }

@@ -614,12 +614,13 @@ def test_flash_attention_q8_0(bridge, oracle, D, M):
     assert torch.isfinite(O).all()
 
 
-@pytest.mark.parametrize("D,M", [(64, 1000), (64, 384), (64, 640), (128, 777)])
+@pytest.mark.parametrize("D,M", [(64, 1000), (64, 384), (64, 640), (128, 777), (128, 384), (128, 640), (128, 2048)])
 def test_flash_attention_many_tiles(bridge, oracle, D, M):
     """Many key tiles per query block: the pipelined K/V staging across tile
     counts, the last partial tile, and (M = 384, 640: an odd number of
     128-query tiles) the middle tile that pairs with itself, both wave groups
-    splitting every key tile of it and merging at the end."""
+    splitting every key tile of it and merging at the end.  Key tiles are 128
+    keys at D = 64 and 64 keys at D = 128 (one unit per group on a split tile)."""
     H = 2
     rng = np.random.default_rng(D + M)
     Q, K, V = (rng.standard_normal((H, M, D)).astype(np.float16) for _ in range(3))
@@ -631,8 +632,9 @@ def test_flash_attention_many_tiles(bridge, oracle, D, M):
     assert maxdiff(host(O), oracle.attention_q8_0(Q, Kq, Vq, scale)) <= TOL
 
 
-def test_flash_attention_negative_scale(bridge, oracle):
-    H, M, D = 2, 200, 64
+@pytest.mark.parametrize("D", [64, 128])
+def test_flash_attention_negative_scale(bridge, oracle, D):
+    H, M = 2, 200
     rng = np.random.default_rng(17)
     Q, K, V = ((rng.standard_normal((H, M, D)) * 0.5).astype(np.float16) for _ in range(3))
     Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
