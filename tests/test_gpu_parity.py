@@ -815,10 +815,11 @@ def test_flash_attention_gqa(bridge, oracle, H, Hkv, M, D):
     assert maxdiff(host(O), ref) <= TOL
 
 
-@pytest.mark.parametrize("norm_type,rope,traditional,Hkv", [(1, True, False, 2), (2, True, True, 4),
-                                                            (1, False, False, 1)])
-def test_prefill_layer_ex(bridge, oracle, norm_type, rope, traditional, Hkv):
-    M, dm, Hq, D, Nm = 160, 256, 4, 64, 512
+@pytest.mark.parametrize("norm_type,rope,traditional,Hq,Hkv,D", [(1, True, False, 4, 2, 64), (2, True, True, 4, 4, 64),
+                                                                  (1, False, False, 4, 1, 64),
+                                                                  (1, True, False, 2, 1, 128)])
+def test_prefill_layer_ex(bridge, oracle, norm_type, rope, traditional, Hq, Hkv, D):
+    M, dm, Nm = 160, 256, 512
     X = synth.activations(M, dm, 71)
     w_attn = (1 + 0.1 * np.random.default_rng(72).standard_normal(dm)).astype(np.float16)
     w_ffn = (1 + 0.1 * np.random.default_rng(73).standard_normal(dm)).astype(np.float16)

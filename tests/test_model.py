@@ -57,11 +57,12 @@ def _host(t):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt,norm_type", [(0, "rmsnorm"), (2, "gemma_add_one")])
-def test_model_prefill_block_by_block(bridge, oracle, fmt, norm_type):
+@pytest.mark.parametrize("fmt,norm_type,Hq,Hkv,D", [(0, "rmsnorm", 4, 2, 64), (2, "gemma_add_one", 4, 2, 64),
+                                                    (0, "rmsnorm", 2, 1, 128)])
+def test_model_prefill_block_by_block(bridge, oracle, fmt, norm_type, Hq, Hkv, D):
     import torch
 
-    cfg = model.EngineConfig(num_layers=2, hidden_dim=256, num_q_heads=4, num_kv_heads=2, head_dim=64,
+    cfg = model.EngineConfig(num_layers=2, hidden_dim=256, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
                              intermediate_dim=512, vocab_size=512, weight_format=fmt, norm_type=norm_type,
                              rope_theta=10000.0)
     m = model.TransformerModel(cfg)
@@ -76,13 +77,13 @@ def test_model_prefill_block_by_block(bridge, oracle, fmt, norm_type):
     assert logits.shape == (80, cfg.vocab_size)
     for layer in m.layers:
         Kq, Vq = layer.kv_q8
-        assert Kq.shape == (2, 80, 68) and Vq.shape == (2, 80, 68)
+        assert Kq.shape == (Hkv, 80, D // 32 * 34) and Vq.shape == (Hkv, 80, D // 32 * 34)
 
     nt = model._NORM_TYPES[norm_type]
     h = m.embedding(torch.as_tensor(tokens))
     np.testing.assert_array_equal(_host(h), _host(m.embedding.weight)[tokens])
     for i, layer in enumerate(m.layers):
-        print(f"model block {i} fmt {fmt}", flush=True)
+        print(f"model block {i} fmt {fmt} D {D}", flush=True)
         x = _host(h)
         h = layer(h)
         ws = [_host(w.weight) for w in (layer.wq, layer.wk, layer.wv, layer.wo, layer.w_gate, layer.w_up,
