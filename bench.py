@@ -515,7 +515,7 @@ def main():
         per["cfg5_swiglu"] = bench_swiglu(b, timer, 2048, 2048, 8192, 50)
     if on("cfg5_attention"):
         per["cfg5_attention"] = bench_attention(b, timer, 32, 2048, 64, 51)
-    if want is not None and "attention_d128" in want:  # Llama-3-8B head width, only when named
+    if on("attention_d128"):  # the same shape at the Llama-3-8B head width
         per["attention_d128"] = bench_attention(b, timer, 32, 2048, 128, 56)
     if on("cfg5_layer"):
         per["cfg5_layer"] = bench_layer(b, timer, 2048, 2048, 32, 64, 8192, 52)
