@@ -801,7 +801,7 @@ def test_rope(bridge, oracle, traditional, H, M, D, offset):
     assert (d > 0).mean() < 0.01
 
 
-@pytest.mark.parametrize("H,Hkv,M,D", [(8, 2, 129, 64), (4, 1, 300, 128), (6, 3, 64, 64)])
+@pytest.mark.parametrize("H,Hkv,M,D", [(8, 2, 129, 64), (4, 1, 300, 128), (6, 3, 64, 64), (4, 2, 1025, 128)])
 def test_flash_attention_gqa(bridge, oracle, H, Hkv, M, D):
     rng = np.random.default_rng(H * Hkv + M)
     Q = (rng.standard_normal((H, M, D)) * 0.5).astype(np.float16)
