@@ -69,6 +69,12 @@ def build(jobs: int = 8, verbose: bool = False, out: Path = OUT, build_dir: Path
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    # A shared library links with undefined symbols; a kernel whose host stub
+    # the compiler dropped would only fail when the library is loaded.
+    u = subprocess.run(["nm", "-u", "-C", str(out)], capture_output=True, text=True)
+    missing = [l.strip() for l in u.stdout.splitlines() if "qr::" in l or "m4_" in l]
+    if missing:
+        raise RuntimeError("undefined library symbols after link:\n" + "\n".join(missing[:20]))
     if verbose:
         print(f"built {out}")
     return out

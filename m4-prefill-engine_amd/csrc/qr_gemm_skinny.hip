@@ -368,6 +368,289 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmParams p, f
     }
 }
 
+// ---- single-kernel streaming projection (no K split) ----
+// A workgroup of 16 wave64s owns 16 output columns over the whole of K, so no
+// two workgroups share an output and no second kernel sums partials:
+//  * the 16 columns' weights are one contiguous byte run of W; it is copied
+//    to LDS first, in address order (padded by 16 bytes per column), by
+//    buffer-load-to-LDS (16 bytes per lane, no register round trip);
+//  * K then advances in NCH chunks of 256 (8 quant groups): each chunk's
+//    activation rows (512 bytes each, two rows per 64-lane copy, the 16-byte
+//    units of row r XOR-swizzled by r mod 16 so the fragment reads of 16 rows
+//    hit distinct banks; rows past M read as zeros) go to a ring of S slots,
+//    S - 1 chunks in flight;
+//  * one barrier per chunk orders every wave's copies of chunk c before the
+//    reads and every wave's reads of chunk c - 1 before the copy of chunk
+//    c + S - 1 into that slot; each wave waits for its own copies with an
+//    immediate vmcnt (copies retire in order);
+//  * every lane's copy offsets and LDS read offsets are formed once; a copy is
+//    one instruction with the chunk's K offset in the scalar soffset field,
+//    and every trip count is a compile-time constant (copy loops with runtime
+//    trip counts issued at about half the rate);
+//  * wave w decodes group w % 8 of the chunk (A operand, Frag<F>) and
+//    multiplies it with the row tiles of half w / 8 (B operand);
+//  * the workgroups of one XCD (blockIdx % 8) start at successive chunks (the
+//    K order is rotated), so the CUs sharing an L2 stream different lines of X;
+//  * the 8 group partials of every output meet in LDS in a fixed order.
+// Each CU reads all of X (M K 2 bytes, from L2) beside its 16 K GB / 32 bytes
+// of W: the trade that removes the split-K partials and their kernel.
+constexpr int kStWaves = 16;
+constexpr int kStThreads = 64 * kStWaves;
+constexpr int kStCols = 16;
+constexpr uint32_t kStKC = 256;               // K per chunk
+constexpr uint32_t kStLdsMax = 160 * 1024;
+
+template <int F, int MT, int NCH>
+struct StShape {
+    static constexpr uint32_t GB = GroupBytes<F>::v;
+    static constexpr uint32_t CB = NCH * 8 * GB;                    // column bytes
+    static constexpr uint32_t WROW = CB + 16;                       // padded column in LDS
+    static constexpr uint32_t WI = (kStCols * WROW / 16 + 63) / 64; // 64-lane copies of W
+    static constexpr uint32_t WPW = (WI + kStWaves - 1) / kStWaves;
+    static constexpr uint32_t WBYTES = WI * 1024;
+    static constexpr uint32_t XI = 8 * MT;                          // copies per chunk (two rows each)
+    static constexpr uint32_t XPW = (XI + kStWaves - 1) / kStWaves;  // copy rounds per chunk
+    static constexpr uint32_t SLOT = XI * 1024;
+    static constexpr uint32_t S0 = WBYTES < kStLdsMax ? (kStLdsMax - WBYTES) / SLOT : 0;
+    static constexpr uint32_t S = S0 > 8 ? 8 : S0;                  // ring depth
+    static constexpr uint32_t RED = 8 * MT * 16 * (kStCols + 4) * 4;
+    static constexpr uint32_t LDS = (WBYTES + S * SLOT) > RED ? WBYTES + S * SLOT : RED;
+};
+
+// s_waitcnt vmcnt(N), N an immediate.
+template <uint32_t N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier that is also a compiler barrier for memory accesses (LDS
+// reads after it stay after it; copies into a freed slot stay after it).
+__device__ __forceinline__ void barrier_mem() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int F, int MT, int NCH>
+__global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p) {
+    using FR = Frag<F>;
+    // The shape's constants as local constexprs: naming a class template's
+    // static members in kernel code made the host pass drop the kernel stub
+    // silently (the library then linked with the kernel undefined).
+    using SH = StShape<F, MT, NCH>;
+    constexpr uint32_t S = SH::S, CB = SH::CB, WROW = SH::WROW, WI = SH::WI, WPW = SH::WPW, WBYTES = SH::WBYTES,
+                       XI = SH::XI, XPW = SH::XPW, SLOT = SH::SLOT;
+    static_assert(S >= 3, "ring of at least three chunks");
+    constexpr int T0 = (MT + 1) / 2;                    // row tiles of wave half 0
+    constexpr uint32_t K = NCH * kStKC;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r16 = lane & 15;
+    const uint32_t M = p.M, N = p.N;
+    const uint32_t n0 = blockIdx.x * kStCols;
+    const uint32_t ncols = min((uint32_t)kStCols, N - n0);
+    const uint32_t start = (blockIdx.x >> 3) % NCH;     // rotated K order per XCD slot
+    uint8_t* const ring = smem + WBYTES;
+
+    // W region: unit u (16 bytes) of column u / (WROW / 16); the pad unit and
+    // the columns past N read as zeros.  Issued first: waiting for chunk 0
+    // waits for it too.
+    {
+        const auto wr = make_rsrc(p.W + (size_t)n0 * CB, ncols * CB);
+        constexpr uint32_t UPC = WROW / 16;
+#pragma unroll
+        for (uint32_t j = 0; j < WPW; j++) {
+            const uint32_t i = (uint32_t)wave + kStWaves * j;
+            const uint32_t u = i * 64 + lane, col = u / UPC, cu = u % UPC;
+            const uint32_t off = (col < ncols && cu + 1 < UPC) ? col * CB + 16u * cu : kOOB;
+            if (i < WI)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(smem + i * 1024u),
+                                                         16, off, 0, 0, 0);
+        }
+    }
+    // X copies: copy i of a chunk holds rows 2i (lanes 0-31) and 2i + 1; lane
+    // unit pu of row r is logical unit pu ^ (r mod 16) of the row's 512 bytes.
+    // The chunk's K offset goes in soffset.
+    const auto xr = make_rsrc(p.X, M * K * 2u);
+    uint32_t xvo[XPW];
+#pragma unroll
+    for (uint32_t j = 0; j < XPW; j++) {
+        const uint32_t i = (uint32_t)wave + kStWaves * j;
+        const uint32_t row = 2u * i + ((uint32_t)lane >> 5);
+        xvo[j] = row < M ? row * K * 2u + 16u * (((uint32_t)lane & 31u) ^ (row & 15u)) : kOOB;
+    }
+    auto kchunk = [&](uint32_t c) { return c + start < NCH ? c + start : c + start - NCH; };
+    auto issue = [&](uint32_t c) {
+        const uint32_t soff = kchunk(c) * kStKC * 2u;
+        uint8_t* const dst = ring + (c % S) * SLOT;
+#pragma unroll
+        for (uint32_t j = 0; j < XPW; j++) {
+            const uint32_t i = (uint32_t)wave + kStWaves * j;
+            const uint32_t vo = xvo[j];  // a local: an array element as the operand made the host pass drop the stub
+            if (i < XI)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(dst + i * 1024u),
+                                                         16, vo, (int)soff, 0, 0);
+        }
+    };
+    // Waves below XI % 16 issue XPW copies per chunk, the others XPW - 1 (XPW
+    // when 16 divides XI).
+    constexpr uint32_t XREM = XI % kStWaves;
+    const bool full = XREM == 0 || (uint32_t)wave < XREM;
+    constexpr uint32_t PRE = S - 1 < NCH ? S - 1 : NCH;
+#pragma unroll
+    for (uint32_t c = 0; c < PRE; c++) issue(c);
+
+    // LDS read offsets of this lane's B fragments (slot-relative) and weights
+    const uint32_t gi = (uint32_t)wave & 7u;            // group of the chunk this wave decodes
+    const int half = wave >> 3;
+    const int t_lo = half ? T0 : 0, t_n = half ? MT - T0 : T0;
+    uint32_t xlo[T0], xhi[T0];
+#pragma unroll
+    for (int t = 0; t < T0; t++) {
+        const uint32_t m = 16u * (t_lo + t) + r16, sw = m & 15u;
+        const uint32_t rowb = (m >> 1) * 1024u + (m & 1u) * 512u;
+        if constexpr (FR::kNibbleOrder) {  // k = 4g .. 4g + 3, 16 + 4g .. 19 + 4g
+            xlo[t] = rowb + 16u * ((4u * gi + ((uint32_t)g >> 1)) ^ sw) + 8u * ((uint32_t)g & 1u);
+            xhi[t] = rowb + 16u * ((4u * gi + 2u + ((uint32_t)g >> 1)) ^ sw) + 8u * ((uint32_t)g & 1u);
+        } else {
+            xlo[t] = rowb + 16u * ((4u * gi + (uint32_t)g) ^ sw);
+            xhi[t] = 0;
+        }
+    }
+    const uint8_t* const strip = smem + (uint32_t)r16 * WROW;
+
+    f4_t acc[T0];
+#pragma unroll
+    for (int t = 0; t < T0; t++) acc[t] = f4_t{};
+#pragma unroll
+    for (uint32_t c = 0; c < NCH; c++) {
+        // chunks issued after c: min(S - 2, NCH - 1 - c), a constant once unrolled
+        constexpr uint32_t AMAX = S - 2;
+        const uint32_t ahead = (NCH - 1 - c) < AMAX ? (NCH - 1 - c) : AMAX;
+#define QR_ST_WAIT(A)                                                                    \
+        if (ahead == (A)) {                                                              \
+            if (full) wait_vmcnt<XPW * (A)>(); else wait_vmcnt<(XPW - 1) * (A)>();       \
+        }
+        QR_ST_WAIT(0) QR_ST_WAIT(1) QR_ST_WAIT(2) QR_ST_WAIT(3) QR_ST_WAIT(4) QR_ST_WAIT(5) QR_ST_WAIT(6)
+#undef QR_ST_WAIT
+        barrier_mem();
+        if (c + S - 1 < NCH) issue(c + S - 1);
+        const uint8_t* const xs = ring + (c % S) * SLOT;
+        const uint32_t kb = kchunk(c) * 8u + gi;         // group within the column
+        uint32_t raw[FR::kRaw];
+        FR::load(strip, kb, g, raw);
+        u4_t xf[T0];
+#pragma unroll
+        for (int t = 0; t < T0; t++) {
+            if (t < t_n) {
+                if constexpr (FR::kNibbleOrder) {
+                    const u2_t lo = *reinterpret_cast<const u2_t*>(xs + xlo[t]);
+                    const u2_t hi = *reinterpret_cast<const u2_t*>(xs + xhi[t]);
+                    xf[t] = u4_t{lo.x, lo.y, hi.x, hi.y};
+                } else {
+                    xf[t] = *reinterpret_cast<const u4_t*>(xs + xlo[t]);
+                }
+            }
+        }
+        const h8_t a = FR::decode(raw, kb, g);
+#pragma unroll
+        for (int t = 0; t < T0; t++)
+            if (t < t_n) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, xf[t]), acc[t], 0, 0, 0);
+    }
+
+    // ---- the 8 group partials of every output through LDS, fixed order ----
+    // red [gi][m][n] with row stride RS = 16 + 4 floats; acc[t] holds
+    // n = 4g + i, m = 16 (t_lo + t) + r16.
+    constexpr int RS = kStCols + 4;
+    constexpr int ROWS = MT * 16;
+    float* red = reinterpret_cast<float*>(smem);
+    barrier_mem();  // every wave is done reading W and the ring (all copies were waited for)
+#pragma unroll
+    for (int t = 0; t < T0; t++)
+        if (t < t_n)
+            *reinterpret_cast<f4_t*>(red + (gi * ROWS + 16 * (t_lo + t) + r16) * RS + 4 * g) = acc[t];
+    __syncthreads();
+    for (uint32_t idx = tid; idx < M * kStCols; idx += kStThreads) {
+        const uint32_t m = idx / kStCols, nl = idx % kStCols;
+        if (nl >= ncols) continue;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) v += red[(w * ROWS + m) * RS + nl];
+        const uint32_t n = n0 + nl;
+        if (p.R) v += (float)p.R[(size_t)m * N + n];
+        size_t o;
+        if (p.head_D) {
+            const uint32_t h = n / p.head_D, dd = n % p.head_D;
+            o = ((size_t)h * M + m) * p.head_D + dd;
+        } else {
+            o = (size_t)m * N + n;
+        }
+        p.Y[o] = (_Float16)v;
+    }
+}
+
+template <int F, int MT, int NCH>
+static hipError_t launch_st(const GemmParams& p, hipStream_t st) {
+    using SH = StShape<F, MT, NCH>;
+    if constexpr (SH::S < 3) {
+        return hipErrorInvalidValue;  // st_plan never picks a shape whose ring does not fit
+    } else {
+        auto kern = gemm_stream_kernel<F, MT, NCH>;
+        if (p.K != NCH * kStKC || p.col_bytes != SH::CB) return hipErrorInvalidValue;
+        static size_t attr[kMaxDevices] = {};
+        hipError_t e = lds_limit_once((const void*)kern, SH::LDS, attr);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, dim3((p.N + kStCols - 1) / kStCols), dim3(kStThreads), SH::LDS, st, p);
+        return hipGetLastError();
+    }
+}
+
+template <int F, int NCH>
+static hipError_t launch_st_m(const GemmParams& p, hipStream_t st) {
+    switch ((p.M + 15) / 16) {
+        case 1: return launch_st<F, 1, NCH>(p, st);
+        case 2: return launch_st<F, 2, NCH>(p, st);
+        case 3: return launch_st<F, 3, NCH>(p, st);
+        case 4: return launch_st<F, 4, NCH>(p, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int F>
+static hipError_t launch_st_k(const GemmParams& p, hipStream_t st) {
+    switch (p.K / kStKC) {
+        case 8: return launch_st_m<F, 8>(p, st);
+        case 16: return launch_st_m<F, 16>(p, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// Ring depth of the shape a (format, M, K) takes, 0 when there is none.
+static uint32_t st_slots(int f, uint32_t M, uint32_t K) {
+    const uint32_t nch = K / kStKC, mt = (M + 15) / 16;
+    if (K % kStKC || (nch != 8 && nch != 16) || mt < 1 || mt > 4) return 0;
+#define QR_ST_S(FF, NN) (mt == 1 ? StShape<FF, 1, NN>::S : mt == 2 ? StShape<FF, 2, NN>::S : mt == 3 ? StShape<FF, 3, NN>::S : StShape<FF, 4, NN>::S)
+#define QR_ST_SF(FF) (nch == 8 ? QR_ST_S(FF, 8) : QR_ST_S(FF, 16))
+    switch (f) {
+        case QUANT_Q4_0: return QR_ST_SF(QUANT_Q4_0);
+        case QUANT_MLX_4BIT: return QR_ST_SF(QUANT_MLX_4BIT);
+        case QUANT_Q4_K: return QR_ST_SF(QUANT_Q4_K);
+        case QUANT_TERNARY_1_58: return QR_ST_SF(QUANT_TERNARY_1_58);
+        case QUANT_MLX_4BIT_G64: return QR_ST_SF(QUANT_MLX_4BIT_G64);
+        default: return 0;
+    }
+#undef QR_ST_SF
+#undef QR_ST_S
+}
+
+// The single-kernel form when its grid of 16-column workgroups covers the
+// 256 CUs without reading X from L2 more than twice per CU, K is 2048 or 4096,
+// and LDS holds the weight strip and a ring of at least 3 chunks.
+static bool st_plan(int f, uint32_t M, uint32_t N, uint32_t K) {
+    if (M == 0 || M > 64) return false;
+    const uint32_t groups = (N + kStCols - 1) / kStCols;
+    if (groups < 256 || groups > 512) return false;
+    return st_slots(f, M, K) >= 3;
+}
+
 static uint32_t group_bytes_rt(int f) {
     switch (f) {
         case QUANT_Q4_0: return GroupBytes<QUANT_Q4_0>::v;
@@ -404,6 +687,7 @@ size_t skinny_workspace_floats(uint32_t M, uint32_t N, uint32_t K) {
     uint32_t ks_max = 1;
     for (int f : {0, 1, 2, 3, (int)QUANT_MLX_4BIT_G64}) {
         uint32_t ks = 1, gpw = 1;
+        if (st_plan(f, M, N, K)) continue;  // single kernel: no partials
         if (sk_plan(f, M, N, K, &ks, &gpw) && ks > ks_max) ks_max = ks;
     }
     return ks_max > 1 ? (size_t)ks_max * M * N : 0;
@@ -439,6 +723,7 @@ static hipError_t launch_sk_g(const GemmParams& p, float* ws, uint32_t ks, uint3
 
 template <int F>
 static hipError_t launch_sk_m(const GemmParams& p, float* ws, hipStream_t st) {
+    if (st_plan(F, p.M, p.N, p.K)) return launch_st_k<F>(p, st);
     uint32_t ks = 0, gpw = 0;
     if (!sk_plan(F, p.M, p.N, p.K, &ks, &gpw)) return hipErrorInvalidValue;
     switch ((p.M + 15) / 16) {
@@ -454,7 +739,7 @@ bool skinny_supported(const GemmParams& p) {
     if (p.W2 || !((p.format >= 0 && p.format <= 3) || p.format == QUANT_MLX_4BIT_G64)) return false;
     if (p.col_bytes % 16) return false;
     uint32_t ks, gpw;
-    return sk_plan(p.format, p.M, p.N, p.K, &ks, &gpw);
+    return st_plan(p.format, p.M, p.N, p.K) || sk_plan(p.format, p.M, p.N, p.K, &ks, &gpw);
 }
 
 hipError_t launch_gemm_skinny(const GemmParams& p, float* ws, hipStream_t st) {

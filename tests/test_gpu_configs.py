@@ -11,10 +11,15 @@ reference verifies each of its bench shapes against its gold the same way
 (bench_universal_router.mm:955; brick4_attn_bench.mm:250-255, 320;
 unified_prefill_engine.mm:702).
 
-Bars: flat max |diff| <= 1/128 for the projections, SwiGLU and attention
-(tolerance.check_ref: one fp16 step where |gold| >= 8); 2/128 for the layer,
-whose fp16 intermediates can flip one step upstream (the reference's own
-layer check allows 0.05, unified_prefill_engine.mm:692).
+Bars: flat max |diff| <= 1/128 for the projections, SwiGLU and attention.
+tolerance.check_ref would allow one fp16 step where |gold| >= 8; on these
+inputs no sampled element reaches |gold| >= 8, and the tests assert that
+count is 0, so every checked element is held to the flat 1/128 bar
+(core/metrology/bench_standards.h:28).  The layer and the full block use
+2/128: a deliberate relaxation, since their fp16 intermediates (and the Q8_0
+KV codes formed from them) can flip one step upstream.  The north-star bar
+does not cover the layer, and the reference's own layer check allows 0.05
+(unified_prefill_engine.mm:692).
 """
 from __future__ import annotations
 
@@ -61,7 +66,8 @@ def run_projection(bridge, oracle, fmt, M, K, N, W, seed, rows=None):
     bridge.synchronize()
     rows = np.arange(M) if rows is None else rows
     ref = oracle.gemm(fmt, np.ascontiguousarray(X[rows]), W, N)
-    tolerance.check_ref(host(Y)[rows], ref, what=f"fmt {fmt} {M}x{K}x{N} ({rows.size} rows)")
+    nbig = tolerance.check_ref(host(Y)[rows], ref, what=f"fmt {fmt} {M}x{K}x{N} ({rows.size} rows)")
+    assert nbig == 0, f"{nbig} elements with |gold| >= 8: the flat 1/128 bar does not cover them"
     return X, Y
 
 
@@ -108,7 +114,8 @@ def test_cfg5_swiglu_m2048_k2048_n8192(bridge, oracle):
     bridge.synchronize()
     rows = sample_rows(M)
     ref = oracle.swiglu(0, np.ascontiguousarray(X[rows]), Wg, Wu, N)
-    tolerance.check_ref(host(out)[rows], ref, what=f"swiglu ({rows.size} rows)")
+    nbig = tolerance.check_ref(host(out)[rows], ref, what=f"swiglu ({rows.size} rows)")
+    assert nbig == 0, f"{nbig} elements with |gold| >= 8: the flat 1/128 bar does not cover them"
 
 
 def test_cfg5_attention_h32_m2048_d64(bridge, oracle):
