@@ -13,7 +13,9 @@ M=33/128/2048, K=4096.  One JSON line on stdout.
   roofline      the dominant kernel of the headline configuration, timed with
                 HIP events on the stream it runs on
   cpu_baseline  the CPU oracle (restated reference gold path) on a bounded row
-                sample of the headline configuration, on this host's cores
+                sample of the headline configuration, on this host's cores;
+                per_config entries of cfg1, cfg3, cfg4, SwiGLU and attention
+                carry their own (half the time budget each)
 
 A step is one projection (or one layer) over one batch.  W untimed warmup
 steps run eagerly; the K timed steps are captured once into a HIP graph and
@@ -211,9 +213,9 @@ def bench_swiglu(b, timer, M, K, N, seed):
 
     import synth
 
-    X = torch.from_numpy(synth.activations(M, K, seed)).cuda()
-    Wg = torch.from_numpy(synth.quantized_weights(0, N, K, seed + 1)).cuda()
-    Wu = torch.from_numpy(synth.quantized_weights(0, N, K, seed + 2)).cuda()
+    Xn, Wgn, Wun = synth.activations(M, K, seed), synth.quantized_weights(0, N, K, seed + 1), \
+        synth.quantized_weights(0, N, K, seed + 2)
+    X, Wg, Wu = (torch.from_numpy(a).cuda() for a in (Xn, Wgn, Wun))
     Out = torch.empty(M, N, dtype=torch.float16, device="cuda")
     lib = b.lib
     # gate + up weights rotate over copies spanning > 512 MB (HBM, not MALL)
@@ -229,16 +231,16 @@ def bench_swiglu(b, timer, M, K, N, seed):
     flops = 4.0 * M * N * K + 4.0 * M * N  # brick3_swiglu_bench.mm:489
     tf = flops / (ms * 1e-3) / 1e12
     return {"name": "swiglu_q4_0", "M": M, "K": K, "N_mlp": N, "ms": round(ms, 5), "tflops": round(tf, 2),
-            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "weight_copies": len(pairs), "timing": timer.mode}
+            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "weight_copies": len(pairs), "timing": timer.mode}, \
+        (Xn, Wgn, Wun)
 
 
 def bench_attention(b, timer, H, M, D, seed):
     import torch
 
     rng = np.random.default_rng(seed)
-    Q = torch.from_numpy(rng.standard_normal((H, M, D)).astype(np.float16)).cuda()
-    Kf = torch.from_numpy(rng.standard_normal((H, M, D)).astype(np.float16)).cuda()
-    Vf = torch.from_numpy(rng.standard_normal((H, M, D)).astype(np.float16)).cuda()
+    Qn, Kn, Vn = (rng.standard_normal((H, M, D)).astype(np.float16) for _ in range(3))
+    Q, Kf, Vf = (torch.from_numpy(a).cuda() for a in (Qn, Kn, Vn))
     nb = H * M * D // 32
     Kq = torch.empty(nb * 34, dtype=torch.uint8, device="cuda")
     Vq = torch.empty(nb * 34, dtype=torch.uint8, device="cuda")
@@ -256,7 +258,7 @@ def bench_attention(b, timer, H, M, D, seed):
     flops = 2.0 * H * M * (M + 1) * D  # brick4_attn_bench.mm:475
     tf = flops / (ms * 1e-3) / 1e12
     return {"name": "flash_attn_q8_0", "H": H, "M": M, "D": D, "ms": round(ms, 5), "tflops": round(tf, 2),
-            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "timing": timer.mode}
+            "frac_mfma": round(tf / PEAK_MFMA_TFLOPS, 4), "timing": timer.mode}, (Qn, Kn, Vn)
 
 
 def bench_layer(b, timer, M, dm, H, D, Nm, seed):
@@ -443,28 +445,79 @@ def probes(b):
     return out
 
 
-def cpu_baseline(fmt, X, Wn, N, seconds: float):
-    """The oracle (CPU restatement of the reference's gold) on a growing row
-    sample of the headline configuration until ~`seconds` of CPU work."""
+def _oracle():
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle_bindings as ob
 
-    threads = ob.threads()
-    M, K = X.shape
-    rows, t_total, done = 1, 0.0, 0
-    # growing row blocks (wrapping over the M rows) until ~`seconds` of CPU work
-    while t_total < seconds:
-        r = min(rows, M)
+    return ob
+
+
+def cpu_rows(run_rows, M: int, seconds: float, row_work=None):
+    """Runs run_rows(rows) on growing, evenly spread row samples of an M-row
+    job until ~`seconds` of CPU work, and extrapolates the time of the whole
+    job by work: rows, or sum(row_work(i)) where rows cost unequal work
+    (causal attention: row i attends i + 1 keys).  Returns (seconds spent,
+    estimated seconds for all M rows, rows run)."""
+    work = (lambda r: float(np.sum(row_work(r)))) if row_work else (lambda r: float(len(r)))
+    full = work(np.arange(M))
+    n, spent, done, rows_run = 1, 0.0, 0.0, 0
+    while spent < seconds:
+        rows = np.unique(np.linspace(0, M - 1, min(n, M)).astype(np.int64))
         t0 = time.perf_counter()
-        ob.gemm(fmt, X[:r], Wn, N, nthreads=threads)
-        t_total += time.perf_counter() - t0
-        done += r
-        rows *= 2
-    tf = 2.0 * done * N * K / t_total / 1e12
-    return {"value": round(tf, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{done} rows (row blocks of the headline projection M={M}, K={K}, N={N}, repeated), "
-                      f"{t_total:.1f} s, double accumulation, one task per row",
-            "ms_full_projection_est": round(t_total / done * M * 1e3, 1)}
+        run_rows(rows)
+        spent += time.perf_counter() - t0
+        done += work(rows)
+        rows_run += len(rows)
+        n *= 2
+    return spent, spent / done * full, rows_run
+
+
+def cpu_entry(value_tf: float, spent: float, est: float, rows: int, what: str, threads: int):
+    return {"value": round(value_tf, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} rows of {what}, evenly spread over M and repeated in growing blocks, "
+                      f"{spent:.1f} s of CPU work, extrapolated to the whole job by its row work; "
+                      f"double accumulation, one task per row",
+            "ms_full_est": round(est * 1e3, 1)}
+
+
+def cpu_projection(fmt, X, Wn, N, seconds: float, what: str):
+    """The oracle (CPU restatement of the reference's gold projection,
+    cpu_gold_reference.h:15-198) on a row sample of a projection."""
+    ob = _oracle()
+    M, K = X.shape
+    threads = ob.threads()
+    spent, est, rows = cpu_rows(lambda r: ob.gemm(fmt, np.ascontiguousarray(X[r]), Wn, N, nthreads=threads), M,
+                                seconds)
+    return cpu_entry(2.0 * M * N * K / est / 1e12, spent, est, rows, what, threads)
+
+
+def cpu_swiglu(X, Wg, Wu, N, seconds: float):
+    """The SwiGLU gold (brick3_swiglu_bench.mm:49-99) on a row sample."""
+    ob = _oracle()
+    M, K = X.shape
+    threads = ob.threads()
+    spent, est, rows = cpu_rows(lambda r: ob.swiglu(0, np.ascontiguousarray(X[r]), Wg, Wu, N, nthreads=threads), M,
+                                seconds)
+    return cpu_entry((4.0 * M * N * K + 4.0 * M * N) / est / 1e12, spent, est, rows,
+                     f"the SwiGLU M={M} K={K} N={N}", threads)
+
+
+def cpu_attention(Q, K, V, seconds: float):
+    """The causal attention gold over the Q8_0 cache (brick4_attn_bench.mm:
+    70-119, on the dequantized K / V as brick4_attn_bench.mm:241-255) on a
+    query-row sample; row i costs i + 1 keys."""
+    ob = _oracle()
+    H, M, D = Q.shape
+    threads = ob.threads()
+    # the Q8_0 cache, dequantized once before timing (the reference's gold
+    # runs on the dequantized K / V)
+    Kd, Vd = (ob.dequantize_q8_0(ob.quantize_q8_0(a)).reshape(H, M, D) for a in (K, V))
+    scale = 1.0 / math.sqrt(D)
+    run = lambda r: ob.attention_rows(np.ascontiguousarray(Q[:, r]), Kd, Vd, r, M, H, scale,  # noqa: E731
+                                      nthreads=threads)
+    spent, est, rows = cpu_rows(run, M, seconds, row_work=lambda r: (np.asarray(r) + 1) * H)
+    return cpu_entry(2.0 * H * M * (M + 1) * D / est / 1e12, spent, est, rows,
+                     f"causal attention H={H} M={M} D={D} (all heads per sampled query row)", threads)
 
 
 def main():
@@ -487,16 +540,20 @@ def main():
 
     per = {}
     head_inputs = None
+    cpu_inputs = {}
     if on("cfg2_mlx_m128"):
         per["cfg2_mlx_m128"], head_inputs = bench_projection(b, timer, "cfg2_mlx_m128", 1, 128, 4096, 14336, 20)
     if on("cfg2_mlx_g64_m128"):
         per["cfg2_mlx_g64_m128"], _ = bench_projection(b, timer, "cfg2_mlx_g64_m128", 8, 128, 4096, 14336, 20)
     if on("cfg1_q4_0_m33"):
-        per["cfg1_q4_0_m33"], _ = bench_projection(b, timer, "cfg1_q4_0_m33", 0, 33, 4096, 4096, 10)
+        per["cfg1_q4_0_m33"], cpu_inputs["cfg1_q4_0_m33"] = bench_projection(b, timer, "cfg1_q4_0_m33", 0, 33, 4096,
+                                                                              4096, 10)
     if on("cfg3_q4_k_m2048"):
-        per["cfg3_q4_k_m2048"], _ = bench_projection(b, timer, "cfg3_q4_k_m2048", 2, 2048, 4096, 4096, 30)
+        per["cfg3_q4_k_m2048"], cpu_inputs["cfg3_q4_k_m2048"] = bench_projection(b, timer, "cfg3_q4_k_m2048", 2, 2048,
+                                                                                  4096, 4096, 30)
     if on("cfg4_ternary_m129"):
-        per["cfg4_ternary_m129"], _ = bench_projection(b, timer, "cfg4_ternary_m129", 3, 129, 2048, 8192, 40)
+        per["cfg4_ternary_m129"], cpu_inputs["cfg4_ternary_m129"] = bench_projection(b, timer, "cfg4_ternary_m129", 3,
+                                                                                      129, 2048, 8192, 40)
     # every router format at the north-star shape M = 2048, K = 4096 (Q4_K is
     # cfg3 above); the 3/5-bit formats only when named
     for fmt, tag in ((0, "q4_0"), (1, "mlx"), (3, "ternary"), (4, "var_rate"), (5, "exl3")):
@@ -512,11 +569,11 @@ def main():
     if want is not None and "copy_calib" in want:
         per["copy_calib"] = bench_copy(timer, 256 << 20)
     if on("cfg5_swiglu"):
-        per["cfg5_swiglu"] = bench_swiglu(b, timer, 2048, 2048, 8192, 50)
+        per["cfg5_swiglu"], cpu_inputs["cfg5_swiglu"] = bench_swiglu(b, timer, 2048, 2048, 8192, 50)
     if on("cfg5_attention"):
-        per["cfg5_attention"] = bench_attention(b, timer, 32, 2048, 64, 51)
+        per["cfg5_attention"], cpu_inputs["cfg5_attention"] = bench_attention(b, timer, 32, 2048, 64, 51)
     if on("attention_d128"):  # the same shape at the Llama-3-8B head width
-        per["attention_d128"] = bench_attention(b, timer, 32, 2048, 128, 56)
+        per["attention_d128"], _ = bench_attention(b, timer, 32, 2048, 128, 56)
     if on("cfg5_layer"):
         per["cfg5_layer"] = bench_layer(b, timer, 2048, 2048, 32, 64, 8192, 52)
     if on("block_full"):
@@ -552,9 +609,23 @@ def main():
     }
     if not a.no_probes:
         out["probes"] = probes(b)
-    if not a.no_cpu_baseline and head_inputs is not None:
-        X, Wn = head_inputs
-        out["cpu_baseline"] = cpu_baseline(1, X, Wn, 14336, a.cpu_seconds)
+    if not a.no_cpu_baseline:
+        # the CPU gold beside each configuration (rank 0, one GPU, bounded samples)
+        if head_inputs is not None:
+            X, Wn = head_inputs
+            out["cpu_baseline"] = cpu_projection(1, X, Wn, 14336, a.cpu_seconds,
+                                                 "the headline MLX projection M=128 K=4096 N=14336")
+            per["cfg2_mlx_m128"]["cpu_baseline"] = out["cpu_baseline"]
+        side = a.cpu_seconds / 2
+        for name, fmt, N in (("cfg1_q4_0_m33", 0, 4096), ("cfg3_q4_k_m2048", 2, 4096), ("cfg4_ternary_m129", 3, 8192)):
+            if name in cpu_inputs:
+                X, Wn = cpu_inputs[name]
+                per[name]["cpu_baseline"] = cpu_projection(fmt, X, Wn, N, side, f"{name} (M={X.shape[0]}, "
+                                                           f"K={X.shape[1]}, N={N})")
+        if "cfg5_swiglu" in cpu_inputs:
+            per["cfg5_swiglu"]["cpu_baseline"] = cpu_swiglu(*cpu_inputs["cfg5_swiglu"], 8192, side)
+        if "cfg5_attention" in cpu_inputs:
+            per["cfg5_attention"]["cpu_baseline"] = cpu_attention(*cpu_inputs["cfg5_attention"], side)
     b.synchronize()
     print(json.dumps(out))
 

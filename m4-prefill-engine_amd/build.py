@@ -21,7 +21,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # once per format (0..8) so its instantiations compile in parallel.
 SOURCES = ([("qr_gemm.hip", f"qr_gemm_f{f}", (f"-DQR_GEMM_FORMAT={f}",)) for f in range(9)] +
            [(s, s.rsplit(".", 1)[0], ()) for s in ("qr_gemm_host.hip", "qr_gemm_skinny.hip", "qr_dequant.hip",
-                                                   "qr_attention.hip", "qr_norm_rope.hip", "qr_probe.hip", "qr_bridge.cpp", "qr_registry.cpp",
+                                                   "qr_attention.hip", "qr_norm_rope.hip", "qr_probe.hip", "qr_bridge.cpp", "qr_host.cpp", "qr_registry.cpp",
                                                    "qr_gguf.cpp")])
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-ffp-contract=on",

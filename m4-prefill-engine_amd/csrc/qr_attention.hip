@@ -311,8 +311,10 @@ __global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p)
     auto qr_ = make_rsrc(p.Q + (size_t)h * head_elems, (uint32_t)(head_elems * 2));
 
     // ---- K / V^T tiles: fetched 3 tiles ahead into registers, written to
-    // the LDS ring 2 tiles ahead.  Keys past Mp read zeros (K) or finite
-    // cache values of the next row (V^T), both masked out. ----
+    // the LDS ring 2 tiles ahead.  Keys past Mp read zeros: for K the offset
+    // runs past the head's cache, for V^T (rows of Mp keys per dim) a chunk
+    // past Mp would be the next dim's first keys, so its offset is made
+    // out of range -- a masked key must not carry an inf or NaN into P V. ----
     struct Raw { u4_t k[KCH], v[VCH]; };
     auto fetch = [&](int t, Raw& r) {
         const int k0 = t * kPKV;
@@ -324,7 +326,8 @@ __global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p)
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
             const int c = tid + NT * i;
-            r.v[i] = ld_b128(vr, (uint32_t)((c / (kPKV / 8)) * Mp + k0 + (c % (kPKV / 8)) * 8) * 2u);
+            const int key = k0 + (c % (kPKV / 8)) * 8;  // Mp is a multiple of 8: whole chunks in or out
+            r.v[i] = ld_b128(vr, key < Mp ? (uint32_t)((c / (kPKV / 8)) * Mp + key) * 2u : kOOB);
         }
     };
     auto kbuf = [&](int slot) { return smem + slot * TILE; };

@@ -44,13 +44,6 @@
 
 namespace qr {
 
-#ifndef QR_RB_STAGES
-#define QR_RB_STAGES 2
-#endif
-#ifndef QR_RB_VPM
-#define QR_RB_VPM 5
-#endif
-
 
 namespace rb {
 
@@ -94,15 +87,13 @@ __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt
 
 }  // namespace rb
 
-#ifndef QR_RB_DUAL_OCC
-#define QR_RB_DUAL_OCC 1
-#endif
-// SPLIT: the instance carries the split-K reduction (its second accumulator
-// set and batched partial loads need registers); the SwiGLU instance without
-// it is sized for QR_RB_DUAL_OCC workgroups per CU, so one workgroup's
-// prologue and epilogue overlap another's main loop.
+// SPLIT: the instance writes split-K partials (the stores are compiled only
+// into the instances that split).  P: weight fetch distance in steps.
+// kVpm: VALU ops scheduled beside each MFMA of a k-slice.
+constexpr int kWeightStages = 2;
+constexpr int kVpm = 5;
 template <int F, int TM, int TN, int NW, int WR, bool DUAL, int P, bool SPLIT>
-__global__ void __launch_bounds__(64 * NW, ((DUAL && !SPLIT) ? QR_RB_DUAL_OCC : 1))
+__global__ void __launch_bounds__(64 * NW, 1)
 gemm_rb_kernel(GemmParams p) {
     using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
     using Dec = Decoder<F>;
@@ -269,7 +260,7 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
             for (int q = 0; q < NM; q++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, QR_RB_VPM, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x002, kVpm, 0);  // VALU
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -450,8 +441,8 @@ gemm_rb_kernel(GemmParams p) {
 template <int F, int TM, int TN, int NW, int WR, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
-    auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, QR_RB_STAGES, true>
-                             : gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, QR_RB_STAGES, false>;
+    auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, kWeightStages, true>
+                             : gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, kWeightStages, false>;
     const size_t lds = C::LDS_BYTES;
     const uint32_t ntm = (p.M + C::BM - 1) / C::BM;
     uint32_t T = ntm * ((p.N + C::BN - 1) / C::BN);

@@ -8,39 +8,26 @@ namespace qr {
 
 // Shapes {TM, TN, NW, WR}: NW waves in WR row groups; BM = 32 TM WR,
 // BN = 32 TN NW / WR.
-//   0 (M >= 1024): QR_RB_BIG  (default 4, 2, 4 -> 128 x 256; Q4_K and ternary:
-//                  QR_RB_BIG_K, default 4, 1, 8 -> 128 x 256 with two waves per
+//   0 (M >= 1024): QR_RB_BIG  (4, 2, 4 -> 128 x 256; Q4_K and ternary:
+//                  QR_RB_BIG_K, 4, 1, 8 -> 128 x 256 with two waves per
 //                  SIMD, whose heavier decode then overlaps the other wave's MFMAs)
-//   1 (M <  1024): QR_RB_MID  (default 4, 1, 4 -> 128 x 128: twice the tiles
+//   1 (M <  1024): QR_RB_MID  (4, 1, 4 -> 128 x 128: twice the tiles
 //                  of 128 x 256 at the same K split, half the reduction)
 //   4 (M <  1024, last 128-row tile at most half full, cheap-decode formats):
-//                  QR_RB_MID64 (default 2, 1, 4 -> 64 x 128: e.g. M = 129
+//                  QR_RB_MID64 (2, 1, 4 -> 64 x 128: e.g. M = 129
 //                  computes 192 rows, not 256)
 //   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
-#ifndef QR_RB_BIG
 #define QR_RB_BIG 4, 2, 4, 1
-#endif
-#ifndef QR_RB_BIG_K
 #define QR_RB_BIG_K 4, 1, 8, 1
-#endif
-#ifndef QR_RB_MID
 #define QR_RB_MID 4, 1, 4, 1
-#endif
-#ifndef QR_RB_MID64
 #define QR_RB_MID64 2, 1, 4, 1
-#endif
-#ifndef QR_RB_DUAL
 #define QR_RB_DUAL 4, 1, 4, 1
-#endif
 template <int TM, int TN, int NW, int WR> struct ShapeOf {
     static constexpr uint32_t bm = 32 * TM * WR, bn = 32 * TN * (NW / WR);
 };
 struct RbShape {
     uint32_t bm, bn;
 };
-#ifndef QR_RB_MID_FILL
-#define QR_RB_MID_FILL 1
-#endif
 // Shape choice.  At M >= 1024 the wide tile is used while it alone fills the
 // 256 CUs; when it cannot (N small), 128 x 128 tiles give twice the tiles, so
 // the K split -- whose fp32 partials are M x N x 4 bytes written and read per
@@ -56,7 +43,7 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
         // (ternary M = 2048: 68-70 us vs 76 us with one wave per SIMD)
         if (format == QUANT_Q4_K || format == QUANT_TERNARY_1_58) return 3;
         const uint32_t big_tiles = ((M + 127) / 128) * ((N + 255) / 256);
-        if (QR_RB_MID_FILL && big_tiles < 256) return 1;
+        if (big_tiles < 256) return 1;
         return 0;
     }
     // 64-row tiles decode every weight twice as often per MFMA: worth it only
@@ -65,10 +52,6 @@ inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
     const bool cheap = format == QUANT_Q4_0 || format == QUANT_MLX_4BIT || format == QUANT_TERNARY_1_58 ||
                        format == QUANT_Q8_0 || format == QUANT_PRISM_Q2_0 || format == QUANT_MLX_4BIT_G64;
     const uint32_t tail = M % 128;
-#ifdef QR_RB_MID64_FILL
-    // 64-row tiles whenever 128-row tiles leave the CUs under-filled
-    if (cheap && ((M + 127) / 128) * ((N + 127) / 128) < 256) return 4;
-#endif
     return (cheap && tail != 0 && tail <= 64) ? 4 : 1;
 }
 inline RbShape rb_dims(int s) {

@@ -35,7 +35,27 @@
 #include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
+#include <stdio.h>
 #include <string.h>
+
+/* Allocation failure: row workers skip their row and raise this flag, which
+ * the exported functions that return a status report as -5; the others stop
+ * with a message (they have no status to return). */
+static int g_alloc_failed = 0;
+static void* row_alloc(size_t n) {
+    void* p = malloc(n ? n : 1);
+    if (!p) __atomic_store_n(&g_alloc_failed, 1, __ATOMIC_RELAXED);
+    return p;
+}
+static void* must_alloc(size_t n) {
+    void* p = malloc(n ? n : 1);
+    if (!p) {
+        fprintf(stderr, "oracle: out of memory allocating %zu bytes\n", n);
+        abort();
+    }
+    return p;
+}
+static int take_alloc_status(void) { return __atomic_exchange_n(&g_alloc_failed, 0, __ATOMIC_RELAXED) ? -5 : 0; }
 
 #define EXPORT __attribute__((visibility("default")))
 
@@ -381,7 +401,8 @@ static double block_dot(int f, const double* w, const double* a) {
 static void gemm_row(void* vctx, size_t m) {
     gemm_ctx* c = (gemm_ctx*)vctx;
     uint32_t bs = kBlockElems[c->f], bb = kBlockBytes[c->f], nb = c->K / bs;
-    double* a = (double*)malloc(sizeof(double) * c->K);
+    double* a = (double*)row_alloc(sizeof(double) * c->K);
+    if (!a) return;
     for (uint32_t k = 0; k < c->K; k++) a[k] = orc_f16_to_f64(c->A[(size_t)m * c->K + k]);
     double w[256];
     for (uint32_t n = 0; n < c->N; n++) {
@@ -413,7 +434,7 @@ EXPORT int orc_gemm(int f, const uint16_t* A, const uint8_t* B, uint16_t* C, con
     if (K % kBlockElems[f]) return -4;
     gemm_ctx c = {f, A, B, C, R, M, N, K, H, D, direct_head, NULL};
     parallel_rows(gemm_row, &c, M, nthreads);
-    return 0;
+    return take_alloc_status();
 }
 
 /* ------------------------------------------------------------------------ */
@@ -428,7 +449,8 @@ typedef struct {
 static void swiglu_row(void* vctx, size_t m) {
     swiglu_ctx* c = (swiglu_ctx*)vctx;
     uint32_t bs = kBlockElems[c->f], bb = kBlockBytes[c->f], nb = c->K / bs;
-    double* a = (double*)malloc(sizeof(double) * c->K);
+    double* a = (double*)row_alloc(sizeof(double) * c->K);
+    if (!a) return;
     for (uint32_t k = 0; k < c->K; k++) a[k] = orc_f16_to_f64(c->A[(size_t)m * c->K + k]);
     double wg[256], wu[256];
     for (uint32_t n = 0; n < c->N; n++) {
@@ -451,7 +473,7 @@ EXPORT int orc_swiglu(int f, const uint16_t* A, const uint8_t* Bg, const uint8_t
     if (K % kBlockElems[f]) return -4;
     swiglu_ctx c = {f, A, Bg, Bu, O, M, N, K};
     parallel_rows(swiglu_row, &c, M, nthreads);
-    return 0;
+    return take_alloc_status();
 }
 
 /* ------------------------------------------------------------------------ */
@@ -511,7 +533,8 @@ static void attn_head_row(void* vctx, size_t idx) {
     size_t MD = (size_t)c->M * c->D;
     size_t hk = h / (c->H / c->Hkv);  /* grouped-query: H / Hkv query heads per KV head */
     const uint16_t* q = c->Q + h * MD + i * c->D;
-    double* s = (double*)malloc(sizeof(double) * (i + 1));
+    double* s = (double*)row_alloc(sizeof(double) * (i + 1));
+    if (!s) return;
     double mx = -1e30;
     for (size_t j = 0; j <= i; j++) {
         const uint16_t* k = c->K + hk * MD + j * c->D;
@@ -541,6 +564,10 @@ EXPORT void orc_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* 
                           int nthreads) {
     attn_ctx c = {Q, K, V, O, H, M, D, (double)scale, o_token_major, H};
     parallel_rows(attn_head_row, &c, (size_t)H * M, nthreads);
+    if (take_alloc_status()) {
+        fprintf(stderr, "oracle: out of memory in orc_attention\n");
+        abort();
+    }
 }
 
 /* Grouped-query attention (src/engine/model.py:234-236 passes Hkv < H heads of
@@ -552,7 +579,7 @@ EXPORT int orc_attention_gqa(const uint16_t* Q, const uint16_t* K, const uint16_
     if (!Hkv || H % Hkv) return -4;
     attn_ctx c = {Q, K, V, O, H, M, D, (double)scale, o_token_major, Hkv};
     parallel_rows(attn_head_row, &c, (size_t)H * M, nthreads);
-    return 0;
+    return take_alloc_status();
 }
 
 /* Row-sampled causal attention: the outputs of query positions pos[0..nr)
@@ -571,7 +598,8 @@ static void attn_rows_row(void* vctx, size_t idx) {
     size_t MD = (size_t)c->M * c->D;
     size_t hk = h / (c->H / c->Hkv);
     const uint16_t* q = c->Q + (h * c->nr + r) * c->D;
-    double* s = (double*)malloc(sizeof(double) * (i + 1));
+    double* s = (double*)row_alloc(sizeof(double) * (i + 1));
+    if (!s) return;
     double mx = -1e30;
     for (size_t j = 0; j <= i; j++) {
         const uint16_t* k = c->K + hk * MD + j * c->D;
@@ -600,7 +628,7 @@ EXPORT int orc_attention_rows(const uint16_t* Qr, const uint16_t* K, const uint1
         if (pos[r] >= M) return -4;
     attn_rows_ctx c = {Qr, K, V, Or, pos, nr, H, Hkv, M, D, (double)scale, o_token_major};
     parallel_rows(attn_rows_row, &c, (size_t)H * nr, nthreads);
-    return 0;
+    return take_alloc_status();
 }
 
 /* Attention over a Q8_0 KV cache: the reference checks its Q8_0 kernel
@@ -610,8 +638,8 @@ EXPORT void orc_attention_q8_0(const uint16_t* Q, const uint8_t* Kq, const uint8
                                uint32_t H, uint32_t M, uint32_t D, float scale, int o_token_major,
                                int nthreads) {
     size_t n = (size_t)H * M * D;
-    uint16_t* Kd = (uint16_t*)malloc(n * 2);
-    uint16_t* Vd = (uint16_t*)malloc(n * 2);
+    uint16_t* Kd = (uint16_t*)must_alloc(n * 2);
+    uint16_t* Vd = (uint16_t*)must_alloc(n * 2);
     orc_dequantize_q8_0(Kq, Kd, n / 32);
     orc_dequantize_q8_0(Vq, Vd, n / 32);
     orc_attention(Q, Kd, Vd, O, H, M, D, scale, o_token_major, nthreads);
@@ -624,8 +652,8 @@ EXPORT int orc_attention_q8_0_gqa(const uint16_t* Q, const uint8_t* Kq, const ui
                                   uint32_t H, uint32_t Hkv, uint32_t M, uint32_t D, float scale,
                                   int o_token_major, int nthreads) {
     size_t n = (size_t)Hkv * M * D;
-    uint16_t* Kd = (uint16_t*)malloc(n * 2);
-    uint16_t* Vd = (uint16_t*)malloc(n * 2);
+    uint16_t* Kd = (uint16_t*)must_alloc(n * 2);
+    uint16_t* Vd = (uint16_t*)must_alloc(n * 2);
     orc_dequantize_q8_0(Kq, Kd, n / 32);
     orc_dequantize_q8_0(Vq, Vd, n / 32);
     int rc = orc_attention_gqa(Q, Kd, Vd, O, H, Hkv, M, D, scale, o_token_major, nthreads);
@@ -716,14 +744,14 @@ EXPORT int orc_layer(int f, const uint16_t* X, const uint8_t* Wq, const uint8_t*
                      uint16_t* Vh, uint16_t* Oattn, uint16_t* Xmid, uint16_t* S, int nthreads) {
     uint32_t HD = H * D;
     size_t nq = (size_t)M * HD;
-    uint16_t* q = Qh ? Qh : (uint16_t*)malloc(nq * 2);
-    uint16_t* k = Kh ? Kh : (uint16_t*)malloc(nq * 2);
-    uint16_t* v = Vh ? Vh : (uint16_t*)malloc(nq * 2);
-    uint16_t* o = Oattn ? Oattn : (uint16_t*)malloc(nq * 2);
-    uint16_t* xm = Xmid ? Xmid : (uint16_t*)malloc((size_t)M * dm * 2);
-    uint16_t* s = S ? S : (uint16_t*)malloc((size_t)M * Nm * 2);
-    uint8_t* kq = (uint8_t*)malloc(nq / 32 * 34);
-    uint8_t* vq = (uint8_t*)malloc(nq / 32 * 34);
+    uint16_t* q = Qh ? Qh : (uint16_t*)must_alloc(nq * 2);
+    uint16_t* k = Kh ? Kh : (uint16_t*)must_alloc(nq * 2);
+    uint16_t* v = Vh ? Vh : (uint16_t*)must_alloc(nq * 2);
+    uint16_t* o = Oattn ? Oattn : (uint16_t*)must_alloc(nq * 2);
+    uint16_t* xm = Xmid ? Xmid : (uint16_t*)must_alloc((size_t)M * dm * 2);
+    uint16_t* s = S ? S : (uint16_t*)must_alloc((size_t)M * Nm * 2);
+    uint8_t* kq = (uint8_t*)must_alloc(nq / 32 * 34);
+    uint8_t* vq = (uint8_t*)must_alloc(nq / 32 * 34);
     int rc = 0;
     rc |= orc_gemm(f, X, Wq, q, NULL, M, HD, dm, 1, H, D, nthreads);
     rc |= orc_gemm(f, X, Wk, k, NULL, M, HD, dm, 1, H, D, nthreads);
@@ -767,15 +795,15 @@ EXPORT int orc_layer_ex(int f, const uint16_t* X, const uint16_t* w_attn, const 
     if (!Hkv || Hq % Hkv) return -4;
     uint32_t HQ = Hq * D, HK = Hkv * D;
     size_t nq = (size_t)M * HQ, nk = (size_t)M * HK;
-    uint16_t* xn = (uint16_t*)malloc((size_t)M * dm * 2);
-    uint16_t* q = (uint16_t*)malloc(nq * 2);
-    uint16_t* k = (uint16_t*)malloc(nk * 2);
-    uint16_t* v = (uint16_t*)malloc(nk * 2);
-    uint16_t* o = (uint16_t*)malloc(nq * 2);
-    uint16_t* xm = (uint16_t*)malloc((size_t)M * dm * 2);
-    uint16_t* s = (uint16_t*)malloc((size_t)M * Nm * 2);
-    uint8_t* kq = (uint8_t*)malloc(nk / 32 * 34);
-    uint8_t* vq = (uint8_t*)malloc(nk / 32 * 34);
+    uint16_t* xn = (uint16_t*)must_alloc((size_t)M * dm * 2);
+    uint16_t* q = (uint16_t*)must_alloc(nq * 2);
+    uint16_t* k = (uint16_t*)must_alloc(nk * 2);
+    uint16_t* v = (uint16_t*)must_alloc(nk * 2);
+    uint16_t* o = (uint16_t*)must_alloc(nq * 2);
+    uint16_t* xm = (uint16_t*)must_alloc((size_t)M * dm * 2);
+    uint16_t* s = (uint16_t*)must_alloc((size_t)M * Nm * 2);
+    uint8_t* kq = (uint8_t*)must_alloc(nk / 32 * 34);
+    uint8_t* vq = (uint8_t*)must_alloc(nk / 32 * 34);
     int rc = 0;
     const uint16_t* a = X;
     if (w_attn) {
@@ -822,18 +850,18 @@ EXPORT int orc_layer_ex_rows(int f, const uint16_t* X, const uint16_t* w_attn, c
         if (pos[r] >= M) return -4;
     uint32_t HQ = Hq * D, HK = Hkv * D;
     size_t nk = (size_t)M * HK;
-    uint16_t* xn = (uint16_t*)malloc((size_t)M * dm * 2);
-    uint16_t* k = (uint16_t*)malloc(nk * 2);
-    uint16_t* v = (uint16_t*)malloc(nk * 2);
-    uint8_t* kq = (uint8_t*)malloc(nk / 32 * 34);
-    uint8_t* vq = (uint8_t*)malloc(nk / 32 * 34);
-    uint16_t* xr = (uint16_t*)malloc((size_t)nr * dm * 2);    /* sampled (normed) rows */
-    uint16_t* x0 = (uint16_t*)malloc((size_t)nr * dm * 2);    /* sampled input rows */
-    uint16_t* q = (uint16_t*)malloc((size_t)nr * HQ * 2);
-    uint16_t* o = (uint16_t*)malloc((size_t)nr * HQ * 2);
-    uint16_t* xm = (uint16_t*)malloc((size_t)nr * dm * 2);
-    uint16_t* xn2 = (uint16_t*)malloc((size_t)nr * dm * 2);
-    uint16_t* s = (uint16_t*)malloc((size_t)nr * Nm * 2);
+    uint16_t* xn = (uint16_t*)must_alloc((size_t)M * dm * 2);
+    uint16_t* k = (uint16_t*)must_alloc(nk * 2);
+    uint16_t* v = (uint16_t*)must_alloc(nk * 2);
+    uint8_t* kq = (uint8_t*)must_alloc(nk / 32 * 34);
+    uint8_t* vq = (uint8_t*)must_alloc(nk / 32 * 34);
+    uint16_t* xr = (uint16_t*)must_alloc((size_t)nr * dm * 2);    /* sampled (normed) rows */
+    uint16_t* x0 = (uint16_t*)must_alloc((size_t)nr * dm * 2);    /* sampled input rows */
+    uint16_t* q = (uint16_t*)must_alloc((size_t)nr * HQ * 2);
+    uint16_t* o = (uint16_t*)must_alloc((size_t)nr * HQ * 2);
+    uint16_t* xm = (uint16_t*)must_alloc((size_t)nr * dm * 2);
+    uint16_t* xn2 = (uint16_t*)must_alloc((size_t)nr * dm * 2);
+    uint16_t* s = (uint16_t*)must_alloc((size_t)nr * Nm * 2);
     int rc = 0;
     const uint16_t* a = X;
     if (w_attn) {

@@ -259,12 +259,18 @@ def attention_q8_0_rows(Qr, Kq, Vq, pos, M: int, Hkv: int, scale: float, o_token
     """Causal attention over the dequantized Q8_0 K/V [Hkv, M, D] for the query
     positions `pos` only.  Qr [H, len(pos), D] holds those queries; the result
     is [H, len(pos), D] (or [len(pos), H*D] token-major)."""
+    return attention_rows(Qr, dequantize_q8_0(Kq), dequantize_q8_0(Vq), pos, M, Hkv, scale, o_token_major, nthreads)
+
+
+def attention_rows(Qr, Kd, Vd, pos, M: int, Hkv: int, scale: float, o_token_major: bool = False,
+                   nthreads: int | None = None) -> np.ndarray:
+    """attention_q8_0_rows on K / V already in fp16 (e.g. dequantized once)."""
     Qr = np.ascontiguousarray(Qr, dtype=np.float16)
     H, nr, D = Qr.shape
     pos = np.ascontiguousarray(pos, dtype=np.uint32)
     assert pos.size == nr
-    Kd = dequantize_q8_0(Kq)
-    Vd = dequantize_q8_0(Vq)
+    Kd = np.ascontiguousarray(Kd, dtype=np.float16)
+    Vd = np.ascontiguousarray(Vd, dtype=np.float16)
     assert Kd.size == Hkv * M * D
     out = np.empty((nr, H * D) if o_token_major else (H, nr, D), np.float16)
     rc = lib().orc_attention_rows(_p(Qr), _p(Kd), _p(Vd), _p(out), _p(pos), nr, H, Hkv, M, D, scale,

@@ -11,11 +11,11 @@ reference verifies each of its bench shapes against its gold the same way
 (bench_universal_router.mm:955; brick4_attn_bench.mm:250-255, 320;
 unified_prefill_engine.mm:702).
 
-Bars: flat max |diff| <= 1/128 for the projections, SwiGLU and attention.
-tolerance.check_ref would allow one fp16 step where |gold| >= 8; on these
-inputs no sampled element reaches |gold| >= 8, and the tests assert that
-count is 0, so every checked element is held to the flat 1/128 bar
-(core/metrology/bench_standards.h:28).  The layer and the full block use
+Bars: flat max |diff| <= 1/128 for the projections, SwiGLU and attention,
+on every checked element (core/metrology/bench_standards.h:28).
+tolerance.check_ref alone would allow one fp16 step where |gold| >= 8; these
+tests also assert the flat bar there (the SwiGLU sample holds two such
+elements, within 0.004 of the gold), so no element gets the wider step.  The layer and the full block use
 2/128: a deliberate relaxation, since their fp16 intermediates (and the Q8_0
 KV codes formed from them) can flip one step upstream.  The north-star bar
 does not cover the layer, and the reference's own layer check allows 0.05
@@ -51,6 +51,10 @@ def empty16(*shape):
     return torch.empty(*shape, dtype=torch.float16, device="cuda")
 
 
+def maxdiff(a, b) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
 def sample_rows(M: int, n: int = 64) -> np.ndarray:
     """>= n rows: both ends, tile edges (32/64/128/256-row tiles) and an even spread."""
     edges = [0, 1, 31, 32, 63, 64, 127, 128, 129, 255, 256, M // 2, M - 2, M - 1]
@@ -66,8 +70,8 @@ def run_projection(bridge, oracle, fmt, M, K, N, W, seed, rows=None):
     bridge.synchronize()
     rows = np.arange(M) if rows is None else rows
     ref = oracle.gemm(fmt, np.ascontiguousarray(X[rows]), W, N)
-    nbig = tolerance.check_ref(host(Y)[rows], ref, what=f"fmt {fmt} {M}x{K}x{N} ({rows.size} rows)")
-    assert nbig == 0, f"{nbig} elements with |gold| >= 8: the flat 1/128 bar does not cover them"
+    tolerance.check_ref(host(Y)[rows], ref, what=f"fmt {fmt} {M}x{K}x{N} ({rows.size} rows)")
+    assert maxdiff(host(Y)[rows], ref) <= TOL  # the flat bar, |gold| >= 8 included
     return X, Y
 
 
@@ -114,8 +118,8 @@ def test_cfg5_swiglu_m2048_k2048_n8192(bridge, oracle):
     bridge.synchronize()
     rows = sample_rows(M)
     ref = oracle.swiglu(0, np.ascontiguousarray(X[rows]), Wg, Wu, N)
-    nbig = tolerance.check_ref(host(out)[rows], ref, what=f"swiglu ({rows.size} rows)")
-    assert nbig == 0, f"{nbig} elements with |gold| >= 8: the flat 1/128 bar does not cover them"
+    tolerance.check_ref(host(out)[rows], ref, what=f"swiglu ({rows.size} rows)")
+    assert maxdiff(host(out)[rows], ref) <= TOL  # the flat bar, |gold| >= 8 included
 
 
 def test_cfg5_attention_h32_m2048_d64(bridge, oracle):

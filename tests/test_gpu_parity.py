@@ -632,6 +632,34 @@ def test_flash_attention_many_tiles(bridge, oracle, D, M):
     assert maxdiff(host(O), oracle.attention_q8_0(Q, Kq, Vq, scale)) <= TOL
 
 
+@pytest.mark.parametrize("M", [64, 192])
+def test_flash_attention_inf_value_stays_in_its_dims(bridge, oracle, M):
+    """A V block with an inf scale at key 0 (dims 32..63 of head 0 all +inf)
+    reaches every output of those dims and no other.  At D = 64 a key tile is
+    128 keys and the cache is padded to 64: with M = 64 or 192 the last tile
+    runs past the padded length, and its masked keys must read zeros, not the
+    first keys of the next dim's V^T row (P = 0 times inf is NaN)."""
+    H, D = 2, 64
+    rng = np.random.default_rng(M + 7)
+    Q, K, V = ((rng.standard_normal((H, M, D)) * 0.5).astype(np.float16) for _ in range(3))
+    Kq, Vq = oracle.quantize_q8_0(K), oracle.quantize_q8_0(V)
+    blk = Vq.reshape(-1, 34)
+    blk[1, 0:2] = np.frombuffer(np.float16(np.inf).tobytes(), np.uint8)  # head 0, key 0, dims 32..63
+    blk[1, 2:] = 1
+    O = empty16(H, M, D)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    print(f"attention inf V M={M}", flush=True)
+    bridge.dispatch_flash_attn_q8_0(dev(Q), dev(Kq), dev(Vq), O, H, M, D, scale)
+    bridge.synchronize()
+    ref = oracle.attention_q8_0(Q, Kq, Vq, scale).astype(np.float64)
+    got = host(O).astype(np.float64)
+    assert np.isposinf(ref[0, :, 32:]).all() and np.isfinite(np.delete(ref[0], np.s_[32:], axis=1)).all()
+    np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref))
+    fin = np.isfinite(ref)
+    assert np.isfinite(got[fin]).all()
+    assert np.abs(got[fin] - ref[fin]).max() <= TOL
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_flash_attention_negative_scale(bridge, oracle, D):
     H, M = 2, 200
