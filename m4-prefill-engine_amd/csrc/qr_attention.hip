@@ -315,6 +315,23 @@ __global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p)
     // runs past the head's cache, for V^T (rows of Mp keys per dim) a chunk
     // past Mp would be the next dim's first keys, so its offset is made
     // out of range -- a masked key must not carry an inf or NaN into P V. ----
+    // V^T chunk c of a tile (16 bytes: 8 keys of one dim row).  An 8-byte
+    // LDS write pass serves 16 lanes on the 32 banks; at D = 64 (16 chunks per
+    // 66-dword row) 16 chunks of one row would put chunks k and k + 8 on the
+    // same banks, so a pass takes 8 chunks each of two adjacent rows (the
+    // second row lands 2 banks over).  At D = 128 (8 chunks per row) one pass
+    // already spans two rows.
+    auto vchunk = [&](int c, int& row, int& ch) {
+        constexpr int CPR = kPKV / 8;
+        if constexpr (CPR == 16) {
+            const int b = c >> 4, l = c & 15;
+            row = 2 * (b >> 1) + (l >> 3);
+            ch = 8 * (b & 1) + (l & 7);
+        } else {
+            row = c / CPR;
+            ch = c % CPR;
+        }
+    };
     struct Raw { u4_t k[KCH], v[VCH]; };
     auto fetch = [&](int t, Raw& r) {
         const int k0 = t * kPKV;
@@ -325,9 +342,10 @@ __global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p)
         }
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
-            const int c = tid + NT * i;
-            const int key = k0 + (c % (kPKV / 8)) * 8;  // Mp is a multiple of 8: whole chunks in or out
-            r.v[i] = ld_b128(vr, key < Mp ? (uint32_t)((c / (kPKV / 8)) * Mp + key) * 2u : kOOB);
+            int vrow, vch;
+            vchunk(tid + NT * i, vrow, vch);
+            const int key = k0 + vch * 8;  // Mp is a multiple of 8: whole chunks in or out
+            r.v[i] = ld_b128(vr, key < Mp ? (uint32_t)(vrow * Mp + key) * 2u : kOOB);
         }
     };
     auto kbuf = [&](int slot) { return smem + slot * TILE; };
@@ -340,8 +358,9 @@ __global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p)
         }
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
-            const int c = tid + NT * i;
-            _Float16* dst = vbuf(slot) + (c / (kPKV / 8)) * VROW + (c % (kPKV / 8)) * 8;
+            int vrow, vch;
+            vchunk(tid + NT * i, vrow, vch);
+            _Float16* dst = vbuf(slot) + vrow * VROW + vch * 8;
             if constexpr (VROW % 8 == 0) {
                 *reinterpret_cast<u4_t*>(dst) = r.v[i];
             } else {  // rows 8-byte aligned only
@@ -732,30 +751,40 @@ __global__ void __launch_bounds__(256 * NG) flash_attn_pipe_kernel(AttnParams p)
         }
 
         // ---- merge group 0's partial state for the heavy queries into group 1's ----
-        constexpr int SW = DT * 16 + 2;
+        // One record of DT * 16 + 2 floats per lane (o, l, m), padded to a
+        // multiple of 4 floats and written as 16-byte vectors: a lane stride
+        // of 4 (mod 8) dwords puts the 16 lanes of a vector access on
+        // distinct banks.
+        constexpr int SW = (DT * 16 + 2 + 3) / 4 * 4 + ((((DT * 16 + 2 + 3) / 4) & 1) ? 0 : 4);
         float* X = reinterpret_cast<float*>(smem);
         static_assert(4 * 64 * SW * 4 <= NBUF * TILE * 2, "merge buffer fits the tile ring");
+        float* x = X + (wq * 64 + lane) * SW;
         if (grp == 0) {
-            float* x = X + (wq * 64 + lane);
     #pragma unroll
             for (int t = 0; t < DT; t++)
     #pragma unroll
-                for (int r = 0; r < 16; r++) x[(t * 16 + r) * 256] = o[t][r];
-            x[(DT * 16) * 256] = l_run;
-            x[(DT * 16 + 1) * 256] = m_run;
+                for (int r = 0; r < 16; r += 4)
+                    *reinterpret_cast<f4_t*>(x + t * 16 + r) = f4_t{o[t][r], o[t][r + 1], o[t][r + 2], o[t][r + 3]};
+            *reinterpret_cast<f2_t*>(x + DT * 16) = f2_t{l_run, m_run};
         }
         __syncthreads();
         if (grp == 1) {
-            const float* x = X + (wq * 64 + lane);
-            const float ma = x[(DT * 16 + 1) * 256];
+            const f2_t lm = *reinterpret_cast<const f2_t*>(x + DT * 16);
+            const float ma = lm.y;
             const float m = fmaxf(ma, m_run);
             const float fa = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - m);
             const float fb = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
     #pragma unroll
             for (int t = 0; t < DT; t++)
     #pragma unroll
-                for (int r = 0; r < 16; r++) o[t][r] = o[t][r] * fb + x[(t * 16 + r) * 256] * fa;
-            const float lh = l_run * fb + x[(DT * 16) * 256] * fa;
+                for (int r = 0; r < 16; r += 4) {
+                    const f4_t v = *reinterpret_cast<const f4_t*>(x + t * 16 + r);
+                    o[t][r] = o[t][r] * fb + v.x * fa;
+                    o[t][r + 1] = o[t][r + 1] * fb + v.y * fa;
+                    o[t][r + 2] = o[t][r + 2] * fb + v.z * fa;
+                    o[t][r + 3] = o[t][r + 3] * fb + v.w * fa;
+                }
+            const float lh = l_run * fb + lm.x * fa;
             const float l = lh + __shfl_xor(lh, 32);
             store(l > 0.0f ? 1.0f / l : 0.0f);
         }
