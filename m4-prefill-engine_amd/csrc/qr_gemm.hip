@@ -66,7 +66,15 @@ struct Cfg {
     static constexpr int XPT = (XCH + NT - 1) / NT;
     static constexpr int LDS_STAGE = BM * kLdsRow;  // halfs
     static constexpr int ACC = TM * NCB * 16;     // accumulator floats per lane
-    static constexpr int EPI_BYTES = NW * 32 * (WN + 4) * 4;  // epilogue staging
+    // Epilogue staging (floats): the 32-column tile j of a wave row starts at
+    // column EJS * j and rows are ERS apart.  The compiler pairs the band's
+    // LDS writes across tiles (TN > 1) or across rows (TN == 1); a pair
+    // distance of 16 (mod 32) words puts a lane's two dwords in opposite bank
+    // halves.  The row distances also keep the 16-byte reads conflict free
+    // whether a read pass serves 8 lanes from 32 banks or 16 lanes from 64.
+    static constexpr int EJS = TN > 1 ? 48 : 32;
+    static constexpr int ERS = TN > 1 ? (EJS * (TN - 1) + 32 + 31) / 32 * 32 : 48;
+    static constexpr int EPI_BYTES = NW * 32 * ERS * 4;
     static constexpr int LDS_BYTES = 3 * LDS_STAGE * 2 > EPI_BYTES ? 3 * LDS_STAGE * 2 : EPI_BYTES;
 };
 
@@ -361,7 +369,7 @@ gemm_rb_kernel(GemmParams p) {
                         (N & 7u) == 0 && (p.head_D & 7u) == 0;
     if (vec_io) {
         constexpr int WC = C::WN;
-        constexpr int ERS = WC + 4;  // padded LDS row (floats)
+        constexpr int ERS = C::ERS, EJS = C::EJS;
         static_assert(NW * 32 * ERS * 4 <= C::LDS_BYTES, "epilogue staging fits the LDS allocation");
         float* E = reinterpret_cast<float*>(lds) + wave * 32 * ERS;
         __syncthreads();  // every wave is done with the X stages
@@ -371,7 +379,7 @@ gemm_rb_kernel(GemmParams p) {
             for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++)
-                    E[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ERS + j * 32 + c32] = value(i, j, r);
+                    E[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ERS + j * EJS + c32] = value(i, j, r);
             __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes done (wave-local region)
             __builtin_amdgcn_wave_barrier();
             constexpr int CHUNKS = 32 * WC / 8;
@@ -381,8 +389,14 @@ gemm_rb_kernel(GemmParams p) {
                 const int m = wrow0 + i * 32 + row;
                 const int n = wcol0 + c8 * 8;
                 if (m < (int)M && n < (int)N) {
-                    const f4_t lo = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8);
-                    const f4_t hi = *reinterpret_cast<const f4_t*>(E + row * ERS + c8 * 8 + 4);
+                    // Half of the lanes of a read pass take their upper four
+                    // columns first (odd rows with one tile per wave, odd
+                    // tiles otherwise), so one pass covers every bank.
+                    const float* e = E + row * ERS + (c8 >> 2) * EJS + (c8 & 3) * 8;
+                    const int sw = (TN == 1 ? row : (c8 >> 2)) & 1;
+                    const f4_t a = *reinterpret_cast<const f4_t*>(e + 4 * sw);
+                    const f4_t b = *reinterpret_cast<const f4_t*>(e + 4 - 4 * sw);
+                    const f4_t lo = sw ? b : a, hi = sw ? a : b;
                     float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
                     if (p.R) {
                         const u4_t rr = *reinterpret_cast<const u4_t*>(p.R + (size_t)m * N + n);
