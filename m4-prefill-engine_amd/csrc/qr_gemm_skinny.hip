@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmParams p, f
 }
 
 // ---- single-kernel streaming projection (no K split) ----
-// A workgroup of 16 wave64s owns 16 output columns over the whole of K, so no
+// A workgroup of 8 wave64s owns 16 output columns over the whole of K, so no
 // two workgroups share an output and no second kernel sums partials:
 //  * the 16 columns' weights are one contiguous byte run of W; it is copied
 //    to LDS first, in address order (padded by 16 bytes per column), by
@@ -387,14 +387,16 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmParams p, f
 //    one instruction with the chunk's K offset in the scalar soffset field,
 //    and every trip count is a compile-time constant (copy loops with runtime
 //    trip counts issued at about half the rate);
-//  * wave w decodes group w % 8 of the chunk (A operand, Frag<F>) and
-//    multiplies it with the row tiles of half w / 8 (B operand);
+//  * wave w decodes group w of the chunk (A operand, Frag<F>) once and
+//    multiplies it with every row tile (B operand): each weight is decoded
+//    once per workgroup (two waves per group doubled the decode VALU per
+//    SIMD, which bounds this loop);
 //  * the workgroups of one XCD (blockIdx % 8) start at successive chunks (the
 //    K order is rotated), so the CUs sharing an L2 stream different lines of X;
 //  * the 8 group partials of every output meet in LDS in a fixed order.
 // Each CU reads all of X (M K 2 bytes, from L2) beside its 16 K GB / 32 bytes
 // of W: the trade that removes the split-K partials and their kernel.
-constexpr int kStWaves = 16;
+constexpr int kStWaves = 8;  // one per quant group of a chunk
 constexpr int kStThreads = 64 * kStWaves;
 constexpr int kStCols = 16;
 constexpr uint32_t kStKC = 256;               // K per chunk
@@ -438,7 +440,6 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
     constexpr uint32_t S = SH::S, CB = SH::CB, WROW = SH::WROW, WI = SH::WI, WPW = SH::WPW, WBYTES = SH::WBYTES,
                        XI = SH::XI, XPW = SH::XPW, SLOT = SH::SLOT;
     static_assert(S >= 3, "ring of at least three chunks");
-    constexpr int T0 = (MT + 1) / 2;                    // row tiles of wave half 0
     constexpr uint32_t K = NCH * kStKC;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
@@ -490,8 +491,8 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
                                                          16, vo, (int)soff, 0, 0);
         }
     };
-    // Waves below XI % 16 issue XPW copies per chunk, the others XPW - 1 (XPW
-    // when 16 divides XI).
+    // Waves below XI % kStWaves issue XPW copies per chunk, the others XPW - 1
+    // (XPW when kStWaves divides XI).
     constexpr uint32_t XREM = XI % kStWaves;
     const bool full = XREM == 0 || (uint32_t)wave < XREM;
     constexpr uint32_t PRE = S - 1 < NCH ? S - 1 : NCH;
@@ -499,13 +500,11 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
     for (uint32_t c = 0; c < PRE; c++) issue(c);
 
     // LDS read offsets of this lane's B fragments (slot-relative) and weights
-    const uint32_t gi = (uint32_t)wave & 7u;            // group of the chunk this wave decodes
-    const int half = wave >> 3;
-    const int t_lo = half ? T0 : 0, t_n = half ? MT - T0 : T0;
-    uint32_t xlo[T0], xhi[T0];
+    const uint32_t gi = (uint32_t)wave;                 // group of the chunk this wave decodes
+    uint32_t xlo[MT], xhi[MT];
 #pragma unroll
-    for (int t = 0; t < T0; t++) {
-        const uint32_t m = 16u * (t_lo + t) + r16, sw = m & 15u;
+    for (int t = 0; t < MT; t++) {
+        const uint32_t m = 16u * t + r16, sw = m & 15u;
         const uint32_t rowb = (m >> 1) * 1024u + (m & 1u) * 512u;
         if constexpr (FR::kNibbleOrder) {  // k = 4g .. 4g + 3, 16 + 4g .. 19 + 4g
             xlo[t] = rowb + 16u * ((4u * gi + ((uint32_t)g >> 1)) ^ sw) + 8u * ((uint32_t)g & 1u);
@@ -517,9 +516,9 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
     }
     const uint8_t* const strip = smem + (uint32_t)r16 * WROW;
 
-    f4_t acc[T0];
+    f4_t acc[MT];
 #pragma unroll
-    for (int t = 0; t < T0; t++) acc[t] = f4_t{};
+    for (int t = 0; t < MT; t++) acc[t] = f4_t{};
 #pragma unroll
     for (uint32_t c = 0; c < NCH; c++) {
         // chunks issued after c: min(S - 2, NCH - 1 - c), a constant once unrolled
@@ -537,36 +536,33 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
         const uint32_t kb = kchunk(c) * 8u + gi;         // group within the column
         uint32_t raw[FR::kRaw];
         FR::load(strip, kb, g, raw);
-        u4_t xf[T0];
+        u4_t xf[MT];
 #pragma unroll
-        for (int t = 0; t < T0; t++) {
-            if (t < t_n) {
-                if constexpr (FR::kNibbleOrder) {
-                    const u2_t lo = *reinterpret_cast<const u2_t*>(xs + xlo[t]);
-                    const u2_t hi = *reinterpret_cast<const u2_t*>(xs + xhi[t]);
-                    xf[t] = u4_t{lo.x, lo.y, hi.x, hi.y};
-                } else {
-                    xf[t] = *reinterpret_cast<const u4_t*>(xs + xlo[t]);
-                }
+        for (int t = 0; t < MT; t++) {
+            if constexpr (FR::kNibbleOrder) {
+                const u2_t lo = *reinterpret_cast<const u2_t*>(xs + xlo[t]);
+                const u2_t hi = *reinterpret_cast<const u2_t*>(xs + xhi[t]);
+                xf[t] = u4_t{lo.x, lo.y, hi.x, hi.y};
+            } else {
+                xf[t] = *reinterpret_cast<const u4_t*>(xs + xlo[t]);
             }
         }
         const h8_t a = FR::decode(raw, kb, g);
 #pragma unroll
-        for (int t = 0; t < T0; t++)
-            if (t < t_n) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, xf[t]), acc[t], 0, 0, 0);
+        for (int t = 0; t < MT; t++)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, xf[t]), acc[t], 0, 0, 0);
     }
 
     // ---- the 8 group partials of every output through LDS, fixed order ----
     // red [gi][m][n] with row stride RS = 16 + 4 floats; acc[t] holds
-    // n = 4g + i, m = 16 (t_lo + t) + r16.
+    // n = 4g + i, m = 16 t + r16.
     constexpr int RS = kStCols + 4;
     constexpr int ROWS = MT * 16;
     float* red = reinterpret_cast<float*>(smem);
     barrier_mem();  // every wave is done reading W and the ring (all copies were waited for)
 #pragma unroll
-    for (int t = 0; t < T0; t++)
-        if (t < t_n)
-            *reinterpret_cast<f4_t*>(red + (gi * ROWS + 16 * (t_lo + t) + r16) * RS + 4 * g) = acc[t];
+    for (int t = 0; t < MT; t++)
+        *reinterpret_cast<f4_t*>(red + (gi * ROWS + 16 * t + r16) * RS + 4 * g) = acc[t];
     __syncthreads();
     for (uint32_t idx = tid; idx < M * kStCols; idx += kStThreads) {
         const uint32_t m = idx / kStCols, nl = idx % kStCols;
