@@ -31,28 +31,28 @@ namespace qr {
 __device__ __forceinline__ uint32_t lds32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
 // A-operand fragment of one 32-element group, read from a weight strip in LDS
-// (16-byte aligned).  Lane group g = lane / 16 holds elements 8g .. 8g+7, or for
-// formats with kNibbleOrder elements 4g .. 4g+3 and 16+4g .. 19+4g.
+// (16-byte aligned).  Lane group g = lane / 16 holds elements 8g .. 8g+7, so
+// the lane's activations are one 16-byte run.  In the 4-bit formats those are
+// nibble g / 2 of code bytes 8 (g & 1) .. 8 (g & 1) + 7 (code byte j holds
+// elements j and 16 + j).
 // load() reads the raw words of one lane from LDS; decode() is lane-local.
 template <int F> struct Frag;
 
-// Q4_0 (18-byte groups, 2-byte aligned): lane group g takes code bytes
-// 4g .. 4g + 3, i.e. elements 4g .. 4g + 3 (low nibbles) and 16 + 4g .. 19 + 4g
-// (high nibbles) -- kNibbleOrder: the activations are read in the same order.
-// Its code dword sits at a wave-uniform byte shift from the aligned pair of
-// dwords read; a third read fetches the dword holding the scale.
+// Q4_0 (18-byte groups, 2-byte aligned): the lane's two code dwords sit at a
+// wave-uniform byte shift from the three aligned dwords read; a fourth read
+// fetches the dword holding the scale.
 template <> struct Frag<QUANT_Q4_0> {
-    static constexpr int kRaw = 3;
-    static constexpr bool kNibbleOrder = true;
-    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[3]) {
-        const uint8_t* p = strip + ((kb * 18u + 2u + 4u * (uint32_t)g) & ~3u);
-        raw[0] = lds32(p); raw[1] = lds32(p + 4);
-        raw[2] = lds32(strip + ((kb * 18u) & ~3u));  // dword holding the scale
+    static constexpr int kRaw = 4;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[4]) {
+        const uint8_t* p = strip + ((kb * 18u + 2u + 8u * ((uint32_t)g & 1u)) & ~3u);
+        raw[0] = lds32(p); raw[1] = lds32(p + 4); raw[2] = lds32(p + 8);
+        raw[3] = lds32(strip + ((kb * 18u) & ~3u));  // dword holding the scale
     }
-    __device__ static h8_t decode(const uint32_t raw[3], uint32_t kb, int) {
-        const uint32_t w = __builtin_amdgcn_alignbyte(raw[1], raw[0], (kb * 18u + 2u) & 2u);
-        const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-        const uint32_t d16 = ((kb * 18u) & 2u) ? (raw[2] >> 16) : (raw[2] & 0xffffu);
+    __device__ static h8_t decode(const uint32_t raw[4], uint32_t kb, int g) {
+        const uint32_t sh = (kb * 18u + 2u) & 2u, ns = 4u * ((uint32_t)g >> 1);
+        const uint32_t lo = (__builtin_amdgcn_alignbyte(raw[1], raw[0], sh) >> ns) & 0x0f0f0f0fu;
+        const uint32_t hi = (__builtin_amdgcn_alignbyte(raw[2], raw[1], sh) >> ns) & 0x0f0f0f0fu;
+        const uint32_t d16 = ((kb * 18u) & 2u) ? (raw[3] >> 16) : (raw[3] & 0xffffu);
         const h2_t d = as_h2(d16 | (d16 << 16));
         u4_t o;
         if (__all(__builtin_fabsf(h2f(d16)) <= kQ4_0FastMaxScale)) {  // fma(q, d, -8d): -8d exact
@@ -71,19 +71,19 @@ template <> struct Frag<QUANT_Q4_0> {
     }
 };
 
-// MLX_4BIT (20-byte groups, dword aligned), nibble order: every lane reads
-// {d, bias} and code dword g (elements 4g .. 4g+3 low, 16+4g .. 19+4g high).
+// MLX_4BIT (20-byte groups, dword aligned): every lane reads {d, bias} and
+// its two code dwords.
 template <> struct Frag<QUANT_MLX_4BIT> {
-    static constexpr bool kNibbleOrder = true;
-    static constexpr int kRaw = 2;
-    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
+    static constexpr int kRaw = 3;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[3]) {
         const uint8_t* p = strip + kb * 20u;
         raw[0] = lds32(p);
-        raw[1] = lds32(p + 4u + 4u * (uint32_t)g);
+        raw[1] = lds32(p + 4u + 8u * ((uint32_t)g & 1u));
+        raw[2] = lds32(p + 8u + 8u * ((uint32_t)g & 1u));
     }
-    __device__ static h8_t decode(const uint32_t raw[2], uint32_t, int) {
-        const uint32_t db = raw[0];
-        const uint32_t lo = raw[1] & 0x0f0f0f0fu, hi = (raw[1] >> 4) & 0x0f0f0f0fu;
+    __device__ static h8_t decode(const uint32_t raw[3], uint32_t, int g) {
+        const uint32_t db = raw[0], ns = 4u * ((uint32_t)g >> 1);
+        const uint32_t lo = (raw[1] >> ns) & 0x0f0f0f0fu, hi = (raw[2] >> ns) & 0x0f0f0f0fu;
         const uint32_t d16 = db & 0xffffu, b16 = db >> 16;
         const h2_t d = as_h2(d16 | (d16 << 16)), bias = as_h2(b16 | (b16 << 16));
         u4_t w = {as_u32(__builtin_elementwise_fma(code_pair<false>(lo), d, bias)),
@@ -95,22 +95,22 @@ template <> struct Frag<QUANT_MLX_4BIT> {
 };
 
 // Q4_K: group kb is sub-block s = kb % 8 of super-block kb / 8.  Every lane
-// reads the 16-byte header and, in nibble order, code dword g of the
-// sub-block (bytes 16s + 4g .. +3).
+// reads the 16-byte header and its two code dwords of the sub-block (bytes
+// 16 + 16s + 8 (g & 1) .. +7).
 template <> struct Frag<QUANT_Q4_K> {
-    static constexpr bool kNibbleOrder = true;
-    static constexpr int kRaw = 5;
-    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[5]) {
+    static constexpr int kRaw = 6;
+    __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[6]) {
         const uint8_t* p = strip + (kb >> 3) * 144u;
         u4_t h = *reinterpret_cast<const u4_t*>(p);
         raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
-        raw[4] = lds32(p + 16u + 16u * (kb & 7u) + 4u * (uint32_t)g);
+        raw[4] = lds32(p + 16u + 16u * (kb & 7u) + 8u * ((uint32_t)g & 1u));
+        raw[5] = lds32(p + 20u + 16u * (kb & 7u) + 8u * ((uint32_t)g & 1u));
     }
     __device__ static int binade(uint32_t h16) {
         int e = (int)((h16 >> 10) & 0x1f);
         return (e < 1 ? 1 : e) - 15;
     }
-    __device__ static h8_t decode(const uint32_t raw[5], uint32_t kb, int) {
+    __device__ static h8_t decode(const uint32_t raw[6], uint32_t kb, int g) {
         const uint32_t s = kb & 7u;
         const uint32_t d16 = raw[0] & 0xffffu, dm16 = raw[0] >> 16;
         const uint64_t s07 = (uint64_t)raw[1] | ((uint64_t)raw[2] << 32);
@@ -122,7 +122,8 @@ template <> struct Frag<QUANT_Q4_K> {
         const float B = h2f(dm16) * (float)mn;
         const int gap = binade(d16) - binade(dm16);
         const bool fast = (A == 0.0f) || (B == 0.0f) || (gap <= 3 && gap >= -7);
-        const uint32_t q0 = raw[4] & 0x0f0f0f0fu, q1 = (raw[4] >> 4) & 0x0f0f0f0fu;
+        const uint32_t ns = 4u * ((uint32_t)g >> 1);
+        const uint32_t q0 = (raw[4] >> ns) & 0x0f0f0f0fu, q1 = (raw[5] >> ns) & 0x0f0f0f0fu;
         u4_t w;
         if (__all(fast)) {  // exact-sum path only when some lane needs it
             w = u4_t{affine_pair_exact(code_pair<false>(q0), A, -B), affine_pair_exact(code_pair<true>(q0), A, -B),
@@ -138,7 +139,6 @@ template <> struct Frag<QUANT_Q4_K> {
 // TERNARY_1_58 (12-byte groups): elements 8g..8g+7 are the 16-bit field
 // 16(g&1) of code word g/2.  w = (1024 + c - 1025) * d, exact.
 template <> struct Frag<QUANT_TERNARY_1_58> {
-    static constexpr bool kNibbleOrder = false;
     static constexpr int kRaw = 2;
     __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
         const uint8_t* p = strip + kb * 12u;
@@ -166,7 +166,6 @@ template <> struct Frag<QUANT_TERNARY_1_58> {
 // kb / 2; lane group g takes code word 4 (kb % 2) + g, i.e. elements
 // 8g .. 8g + 7 of the group, in element order (two byte permutes).
 template <> struct Frag<QUANT_MLX_4BIT_G64> {
-    static constexpr bool kNibbleOrder = false;
     static constexpr int kRaw = 2;
     __device__ static void load(const uint8_t* strip, uint32_t kb, int g, uint32_t raw[2]) {
         const uint8_t* p = strip + (kb >> 1) * 36u;
@@ -291,13 +290,7 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmParams p, f
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t m = min(16u * mt + r16, M - 1);  // rows >= M are zeroed below
-            if constexpr (FR::kNibbleOrder) {  // k = 4g .. 4g + 3, 16 + 4g .. 19 + 4g
-                const uint8_t* px = xs + m * L.xrs + (kb * 32u + 4u * g) * 2u;
-                const u2_t lo = *reinterpret_cast<const u2_t*>(px), hi = *reinterpret_cast<const u2_t*>(px + 32);
-                xf[b][mt] = u4_t{lo.x, lo.y, hi.x, hi.y};
-            } else {  // k = 8g .. 8g + 7
-                xf[b][mt] = *reinterpret_cast<const u4_t*>(xs + m * L.xrs + (kb * 32u + 8u * g) * 2u);
-            }
+            xf[b][mt] = *reinterpret_cast<const u4_t*>(xs + m * L.xrs + (kb * 32u + 8u * g) * 2u);  // k = 8g .. 8g + 7
         }
 #pragma unroll
         for (int t = 0; t < kSkNT; t++) FR::load(wsb + (16u * t + r16) * L.sbp, kb, g, raw[b][t]);
@@ -377,8 +370,8 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmParams p, f
 //  * K then advances in NCH chunks of 256 (8 quant groups): each chunk's
 //    activation rows (512 bytes each, two rows per 64-lane copy, the 16-byte
 //    units of row r XOR-swizzled by r mod 16 so the fragment reads of 16 rows
-//    hit distinct banks; rows past M read as zeros) go to a ring of S slots,
-//    S - 1 chunks in flight;
+//    hit distinct banks; rows past M are copied as zeros and their lanes read
+//    no fragment) go to a ring of S slots, S - 1 chunks in flight;
 //  * one barrier per chunk orders every wave's copies of chunk c before the
 //    reads and every wave's reads of chunk c - 1 before the copy of chunk
 //    c + S - 1 into that slot; each wave waits for its own copies with an
@@ -501,18 +494,13 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
 
     // LDS read offsets of this lane's B fragments (slot-relative) and weights
     const uint32_t gi = (uint32_t)wave;                 // group of the chunk this wave decodes
-    uint32_t xlo[MT], xhi[MT];
+    // Elements 8g .. 8g + 7 of the group are 16-byte unit 4 gi + g of the row
+    // (swizzled): 8 (or 16) lanes of one read pass hit 8 (16) distinct units.
+    uint32_t xo[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) {
-        const uint32_t m = 16u * t + r16, sw = m & 15u;
-        const uint32_t rowb = (m >> 1) * 1024u + (m & 1u) * 512u;
-        if constexpr (FR::kNibbleOrder) {  // k = 4g .. 4g + 3, 16 + 4g .. 19 + 4g
-            xlo[t] = rowb + 16u * ((4u * gi + ((uint32_t)g >> 1)) ^ sw) + 8u * ((uint32_t)g & 1u);
-            xhi[t] = rowb + 16u * ((4u * gi + 2u + ((uint32_t)g >> 1)) ^ sw) + 8u * ((uint32_t)g & 1u);
-        } else {
-            xlo[t] = rowb + 16u * ((4u * gi + (uint32_t)g) ^ sw);
-            xhi[t] = 0;
-        }
+        const uint32_t m = 16u * t + r16;
+        xo[t] = (m >> 1) * 1024u + (m & 1u) * 512u + 16u * ((4u * gi + (uint32_t)g) ^ (m & 15u));
     }
     const uint8_t* const strip = smem + (uint32_t)r16 * WROW;
 
@@ -538,15 +526,8 @@ __global__ void __launch_bounds__(kStThreads, 1) gemm_stream_kernel(GemmParams p
         FR::load(strip, kb, g, raw);
         u4_t xf[MT];
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-            if constexpr (FR::kNibbleOrder) {
-                const u2_t lo = *reinterpret_cast<const u2_t*>(xs + xlo[t]);
-                const u2_t hi = *reinterpret_cast<const u2_t*>(xs + xhi[t]);
-                xf[t] = u4_t{lo.x, lo.y, hi.x, hi.y};
-            } else {
-                xf[t] = *reinterpret_cast<const u4_t*>(xs + xlo[t]);
-            }
-        }
+        for (int t = 0; t < MT; t++)  // rows past M are zeros: their lanes skip the read
+            xf[t] = 16u * t + r16 < M ? *reinterpret_cast<const u4_t*>(xs + xo[t]) : u4_t{0, 0, 0, 0};
         const h8_t a = FR::decode(raw, kb, g);
 #pragma unroll
         for (int t = 0; t < MT; t++)
