@@ -65,6 +65,15 @@ struct Cfg {
     static constexpr int XCH = BM * kBK / 8;      // 16-byte X chunks per step
     static constexpr int XPT = (XCH + NT - 1) / NT;
     static constexpr int LDS_STAGE = BM * kLdsRow;  // halfs
+    // X staging: with one 32-column tile per wave and no SwiGLU pair (the
+    // instances that leave registers for a fifth wave), an extra stager wave
+    // copies X to LDS (XST: 6 stages, XD steps ahead); otherwise every wave
+    // fetches X into registers and writes it to a 3-stage ring.
+    static constexpr bool XST = !DUAL && TN == 1;
+    static constexpr int NTL = NT + (XST ? 64 : 0);  // threads per workgroup
+    static constexpr int XS = XST ? 6 : 3;
+    static constexpr int XD = 5;
+    static constexpr int XCP = BM * (kLdsRow / 8) / 64;  // 64-lane copies per stage (pad units included)
     static constexpr int ACC = TM * NCB * 16;     // accumulator floats per lane
     // Epilogue staging (floats): the 32-column tile j of a wave row starts at
     // column EJS * j and rows are ERS apart.  The compiler pairs the band's
@@ -75,7 +84,7 @@ struct Cfg {
     static constexpr int EJS = TN > 1 ? 48 : 32;
     static constexpr int ERS = TN > 1 ? (EJS * (TN - 1) + 32 + 31) / 32 * 32 : 48;
     static constexpr int EPI_BYTES = NW * 32 * ERS * 4;
-    static constexpr int LDS_BYTES = 3 * LDS_STAGE * 2 > EPI_BYTES ? 3 * LDS_STAGE * 2 : EPI_BYTES;
+    static constexpr int LDS_BYTES = XS * LDS_STAGE * 2 > EPI_BYTES ? XS * LDS_STAGE * 2 : EPI_BYTES;
 };
 
 __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t gm_req, uint32_t& tm,
@@ -100,8 +109,15 @@ __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt
 // kVpm: VALU ops scheduled beside each MFMA of a k-slice.
 constexpr int kWeightStages = 2;
 constexpr int kVpm = 5;
+// s_waitcnt vmcnt(N), N an immediate.
+template <uint32_t N>
+__device__ __forceinline__ void rb_wait_vmcnt() {
+    static_assert(N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 template <int F, int TM, int TN, int NW, int WR, bool DUAL, int P, bool SPLIT>
-__global__ void __launch_bounds__(64 * NW, 1)
+__global__ void __launch_bounds__(64 * NW + (!DUAL && TN == 1 ? 64 : 0), 1)
 gemm_rb_kernel(GemmParams p) {
     using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
     using Dec = Decoder<F>;
@@ -149,6 +165,50 @@ gemm_rb_kernel(GemmParams p) {
     const int mrows = min(C::BM, (int)M - m0);
     const int ncols = min(C::BN, (int)N - n0);
     auto xr = make_rsrc(p.X + (size_t)m0 * K, (uint32_t)mrows * K * 2u);
+    // ---- X stager (XST): the extra wave NW copies each step's BM x 64 slice of X
+    // into an LDS stage (rows of kLdsRow halfs: 8 16-byte units and a pad
+    // unit, copied as zeros) by buffer-load-to-LDS, XD steps ahead, through
+    // a ring of XS stages; the compute waves never touch X in memory.  Before
+    // the barrier that opens step t it waits (its own copies, in order) for
+    // the copies of step t + 1, whose first k-slice the compute waves read
+    // during step t; after it, stage (t + XD) % XS = (t - 1) % XS is free. It
+    // leaves after the barrier of the last step (a finished wave no longer
+    // holds barriers). ----
+    if (C::XST && wave == NW) {
+        constexpr int UPR = kLdsRow / 8;  // 16-byte units per LDS row
+        uint32_t xo[C::XCP], xh[C::XCP];  // per-lane offsets: whole step, first half (a 32-K last step)
+#pragma unroll
+        for (int q = 0; q < C::XCP; q++) {
+            const uint32_t u = 64u * q + lane, row = u / UPR, cu = u % UPR;
+            const bool live = cu < 8 && row < (uint32_t)mrows;
+            xo[q] = live ? (row * K + 8u * cu) * 2u : kOOB;
+            xh[q] = cu < 4 ? xo[q] : kOOB;
+        }
+        auto issue = [&](uint32_t t) {
+            const uint32_t soff = (k_begin + t * kBK) * 2u;
+            const bool half = k_begin + t * kBK + kBK > k_end;
+            _Float16* const dst = lds + (t % C::XS) * C::LDS_STAGE;
+#pragma unroll
+            for (int q = 0; q < C::XCP; q++) {
+                const uint32_t vo = half ? xh[q] : xo[q];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(dst + q * 512),
+                                                         16, vo, (int)soff, 0, 0);
+            }
+        };
+        for (uint32_t t = 0; t < (uint32_t)C::XD && t < nsteps; t++) issue(t);
+        for (uint32_t t = 0; t < nsteps; t++) {
+            // copies issued after step t + 1's: steps t + 2 .. min(t + XD - 1, nsteps - 1)
+            const int r = min((int)C::XD - 2, (int)nsteps - 2 - (int)t);
+            if (r >= 3) rb_wait_vmcnt<3 * C::XCP>();
+            else if (r == 2) rb_wait_vmcnt<2 * C::XCP>();
+            else if (r == 1) rb_wait_vmcnt<C::XCP>();
+            else rb_wait_vmcnt<0>();
+            asm volatile("s_barrier" ::: "memory");
+            if (t + C::XD < nsteps) issue(t + C::XD);
+        }
+        return;
+    }
+    static_assert(!C::XST || (C::XD - 2 <= 3 && 3 * C::XCP < 64), "stager waits");
     auto wr0 = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
     auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
 
@@ -156,28 +216,31 @@ gemm_rb_kernel(GemmParams p) {
     auto bcol = [&](int jb) { return wcolg * C::WN + (jb % TN) * 32 + c32; };
 
     // Pipelines (U = 6 steps unrolled, so every ring index below is static):
-    //  X:  raw 16-byte chunks fetched 4 steps ahead into XP = 2 register slots,
+    //  X:  (XST) in LDS stage step % XS, copied there by the stager wave; or
+    //      raw 16-byte chunks fetched 4 steps ahead into XP = 2 register slots,
     //      written to LDS 2 steps ahead into a 3-stage ring;
     //  A:  fragments of slice kk + 1 read while slice kk multiplies; the first
     //      slice of step s + 1 is read before the step's barrier (its stage was
     //      written before the previous barrier);
     //  W:  raw blocks fetched WP steps ahead, decoded one step ahead into the
     //      two B buffers.
-    constexpr int XS = 3, XP = 2, WP = P, U = 6;
+    constexpr int XS = C::XS, XP = 2, WP = P, U = 6;
     static_assert(U % XS == 0 && U % XP == 0 && U % WP == 0, "ring sizes divide the unroll");
-    uint32_t xraw[XP][C::XPT][4];
+    uint32_t xraw[XP][C::XST ? 1 : C::XPT][4];
     uint32_t wraw[WP][NCB][Dec::kRawWords];
 
     auto load_x = [&](uint32_t step, int slot) {
-        const uint32_t k0 = k_begin + step * kBK;
+        if constexpr (!C::XST) {
+            const uint32_t k0 = k_begin + step * kBK;
 #pragma unroll
-        for (int i = 0; i < C::XPT; i++) {
-            const int c = tid + NT * i;
-            const int row = c >> 3, kc = c & 7;
-            const uint32_t k = k0 + kc * 8;  // past the range (or the last step): zeros
-            const uint32_t off = ((C::XCH % NT == 0 || c < C::XCH) && k < k_end) ? ((uint32_t)row * K + k) * 2u : kOOB;
-            const u4_t v = ld_b128(xr, off);
-            xraw[slot][i][0] = v.x; xraw[slot][i][1] = v.y; xraw[slot][i][2] = v.z; xraw[slot][i][3] = v.w;
+            for (int i = 0; i < C::XPT; i++) {
+                const int c = tid + NT * i;
+                const int row = c >> 3, kc = c & 7;
+                const uint32_t k = k0 + kc * 8;  // past the range (or the last step): zeros
+                const uint32_t off = ((C::XCH % NT == 0 || c < C::XCH) && k < k_end) ? ((uint32_t)row * K + k) * 2u : kOOB;
+                const u4_t v = ld_b128(xr, off);
+                xraw[slot][i][0] = v.x; xraw[slot][i][1] = v.y; xraw[slot][i][2] = v.z; xraw[slot][i][3] = v.w;
+            }
         }
     };
     auto load_w = [&](uint32_t step, int slot) {
@@ -191,14 +254,16 @@ gemm_rb_kernel(GemmParams p) {
     };
 
     auto store_x = [&](int slot, int stage) {
-        _Float16* As = lds + stage * C::LDS_STAGE;
+        if constexpr (!C::XST) {
+            _Float16* As = lds + stage * C::LDS_STAGE;
 #pragma unroll
-        for (int i = 0; i < C::XPT; i++) {
-            const int c = tid + NT * i;
-            if (C::XCH % NT == 0 || c < C::XCH) {
-                const int row = c >> 3, kc = c & 7;
-                *reinterpret_cast<u4_t*>(As + row * kLdsRow + kc * 8) =
-                    u4_t{xraw[slot][i][0], xraw[slot][i][1], xraw[slot][i][2], xraw[slot][i][3]};
+            for (int i = 0; i < C::XPT; i++) {
+                const int c = tid + NT * i;
+                if (C::XCH % NT == 0 || c < C::XCH) {
+                    const int row = c >> 3, kc = c & 7;
+                    *reinterpret_cast<u4_t*>(As + row * kLdsRow + kc * 8) =
+                        u4_t{xraw[slot][i][0], xraw[slot][i][1], xraw[slot][i][2], xraw[slot][i][3]};
+                }
             }
         }
     };
@@ -462,7 +527,10 @@ static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     uint32_t T = ntm * ((p.N + C::BN - 1) / C::BN);
     for (uint32_t g = 1; g < p.ngroups && g < 3; g++) T += ntm * ((p.Nx[g - 1] + C::BN - 1) / C::BN);
     const uint32_t ks = p.ksplit ? p.ksplit : 1;
-    hipLaunchKernelGGL(kern, dim3(T, ks), dim3(C::NT), lds, st, p);
+    static size_t attr[2][kMaxDevices] = {};
+    const hipError_t e = lds_limit_once((const void*)kern, lds, attr[p.ksplit > 1]);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(T, ks), dim3(C::NTL), lds, st, p);
     return hipGetLastError();
 }
 
