@@ -50,13 +50,14 @@ namespace rb {
 constexpr int kBK = 64;
 constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
 
-// NW waves as WR row groups x NW / WR column groups; a wave's tile is
-// 32 TM rows x 32 TN columns.
-template <int TM, int TN, int NW, int WR, bool DUAL>
+// NW waves as KG K groups of WR row groups x NW / (WR KG) column groups; a
+// wave's tile is 32 TM rows x 32 TN columns.  With KG = 2 the groups take
+// alternate K steps of the whole K range and sum their tiles in LDS at the end.
+template <int TM, int TN, int NW, int WR, int KG, bool DUAL>
 struct Cfg {
-    static_assert(NW % WR == 0, "whole column groups");
+    static_assert(NW % (WR * KG) == 0, "whole column groups");
     static constexpr int NT = 64 * NW;
-    static constexpr int WC = NW / WR;            // column groups
+    static constexpr int WC = NW / (WR * KG);     // column groups
     static constexpr int WM = 32 * TM;            // rows per wave
     static constexpr int BM = WR * WM;
     static constexpr int WN = 32 * TN;            // columns per wave
@@ -71,8 +72,10 @@ struct Cfg {
     // fetches X into registers and writes it to a 3-stage ring.
     static constexpr bool XST = !DUAL && TN == 1;
     static constexpr int NTL = NT + (XST ? 64 : 0);  // threads per workgroup
-    static constexpr int XS = XST ? 6 : 3;
-    static constexpr int XD = 5;
+    static_assert(KG == 1 || XST, "K groups take X from the stager");
+    static constexpr int XD = KG > 1 ? 3 : 5;                // rounds of KG steps the copies run ahead
+    static constexpr int XS = XST ? KG * (XD + 1) : 3;       // X stages in LDS
+    static constexpr int U = KG > 1 ? 4 : 6;                 // rounds unrolled (ring indices static)
     static constexpr int XCP = BM * (kLdsRow / 8) / 64;  // 64-lane copies per stage (pad units included)
     static constexpr int ACC = TM * NCB * 16;     // accumulator floats per lane
     // Epilogue staging (floats): the 32-column tile j of a wave row starts at
@@ -84,7 +87,9 @@ struct Cfg {
     static constexpr int EJS = TN > 1 ? 48 : 32;
     static constexpr int ERS = TN > 1 ? (EJS * (TN - 1) + 32 + 31) / 32 * 32 : 48;
     static constexpr int EPI_BYTES = NW * 32 * ERS * 4;
-    static constexpr int LDS_BYTES = XS * LDS_STAGE * 2 > EPI_BYTES ? XS * LDS_STAGE * 2 : EPI_BYTES;
+    static constexpr int XCH_BYTES = KG > 1 ? NW / KG * ACC * 64 * 4 : 0;  // K-group exchange
+    static constexpr int LDS_BYTES0 = XS * LDS_STAGE * 2 > EPI_BYTES ? XS * LDS_STAGE * 2 : EPI_BYTES;
+    static constexpr int LDS_BYTES = LDS_BYTES0 > XCH_BYTES ? LDS_BYTES0 : XCH_BYTES;
 };
 
 __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t gm_req, uint32_t& tm,
@@ -116,10 +121,11 @@ __device__ __forceinline__ void rb_wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int F, int TM, int TN, int NW, int WR, bool DUAL, int P, bool SPLIT>
+template <int F, int TM, int TN, int NW, int WR, int KG, bool DUAL, int P, bool SPLIT>
 __global__ void __launch_bounds__(64 * NW + (!DUAL && TN == 1 ? 64 : 0), 1)
 gemm_rb_kernel(GemmParams p) {
-    using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
+    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL>;
+    static_assert(!(SPLIT && KG > 1), "K groups replace the K split");
     using Dec = Decoder<F>;
     constexpr int NT = C::NT;
     constexpr int NCB = C::NCB;
@@ -130,7 +136,8 @@ gemm_rb_kernel(GemmParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-    const int wrow = wave / C::WC, wcolg = wave % C::WC;  // this wave's row group and column group
+    const int kg = KG > 1 ? wave / (NW / KG) : 0, wl = KG > 1 ? wave % (NW / KG) : wave;  // K group, wave in it
+    const int wrow = wl / C::WC, wcolg = wl % C::WC;       // this wave's row group and column group
     const int h = lane >> 5;     // quant group of the step this lane owns
     const int c32 = lane & 31;
 
@@ -173,7 +180,8 @@ gemm_rb_kernel(GemmParams p) {
     // the copies of step t + 1, whose first k-slice the compute waves read
     // during step t; after it, stage (t + XD) % XS = (t - 1) % XS is free. It
     // leaves after the barrier of the last step (a finished wave no longer
-    // holds barriers). ----
+    // holds barriers).  With K groups a round is KG consecutive steps, one
+    // per group, and the same holds per round. ----
     if (C::XST && wave == NW) {
         constexpr int UPR = kLdsRow / 8;  // 16-byte units per LDS row
         uint32_t xo[C::XCP], xh[C::XCP];  // per-lane offsets: whole step, first half (a 32-K last step)
@@ -195,20 +203,24 @@ gemm_rb_kernel(GemmParams p) {
                                                          16, vo, (int)soff, 0, 0);
             }
         };
-        for (uint32_t t = 0; t < (uint32_t)C::XD && t < nsteps; t++) issue(t);
-        for (uint32_t t = 0; t < nsteps; t++) {
-            // copies issued after step t + 1's: steps t + 2 .. min(t + XD - 1, nsteps - 1)
-            const int r = min((int)C::XD - 2, (int)nsteps - 2 - (int)t);
+        for (uint32_t t = 0; t < (uint32_t)(KG * C::XD) && t < nsteps; t++) issue(t);
+        const uint32_t nloc = nsteps / KG;
+        for (uint32_t t = 0; t < nloc; t++) {
+            // the barrier opening round t needs steps .. KG (t + 2) - 1; copies
+            // issued after those: steps KG (t + 2) .. min(KG (t + XD) - 1, nsteps - 1)
+            const int r = min(KG * (C::XD - 2), (int)nsteps - KG * ((int)t + 2));
             if (r >= 3) rb_wait_vmcnt<3 * C::XCP>();
             else if (r == 2) rb_wait_vmcnt<2 * C::XCP>();
             else if (r == 1) rb_wait_vmcnt<C::XCP>();
             else rb_wait_vmcnt<0>();
             asm volatile("s_barrier" ::: "memory");
-            if (t + C::XD < nsteps) issue(t + C::XD);
+#pragma unroll
+            for (int i = 0; i < KG; i++)
+                if (KG * (t + C::XD) + i < nsteps) issue(KG * (t + C::XD) + i);
         }
         return;
     }
-    static_assert(!C::XST || (C::XD - 2 <= 3 && 3 * C::XCP < 64), "stager waits");
+    static_assert(!C::XST || (KG * (C::XD - 2) <= 3 && 3 * C::XCP < 64), "stager waits");
     auto wr0 = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
     auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
 
@@ -224,8 +236,8 @@ gemm_rb_kernel(GemmParams p) {
     //      written before the previous barrier);
     //  W:  raw blocks fetched WP steps ahead, decoded one step ahead into the
     //      two B buffers.
-    constexpr int XS = C::XS, XP = 2, WP = P, U = 6;
-    static_assert(U % XS == 0 && U % XP == 0 && U % WP == 0, "ring sizes divide the unroll");
+    constexpr int XS = C::XS, XP = 2, WP = P, U = C::U;
+    static_assert((KG * U) % XS == 0 && U % XP == 0 && U % WP == 0, "ring sizes divide the unroll");
     uint32_t xraw[XP][C::XST ? 1 : C::XPT][4];
     uint32_t wraw[WP][NCB][Dec::kRawWords];
 
@@ -285,8 +297,9 @@ gemm_rb_kernel(GemmParams p) {
 
     const int arow = wrow * C::WM + c32;
     const int akof = 32 * h;
-    auto read_a = [&](int stage, int kk, h8_t out[TM]) {
-        const _Float16* As = lds + stage * C::LDS_STAGE;
+    // stage of local round j (static within the unroll) plus the K group
+    auto read_a = [&](int j, int kk, h8_t out[TM]) {
+        const _Float16* As = lds + ((KG * j) % XS + kg) * C::LDS_STAGE;
 #pragma unroll
         for (int i = 0; i < TM; i++)
             out[i] = *reinterpret_cast<const h8_t*>(As + (arow + i * 32) * kLdsRow + akof + kk * 8);
@@ -307,12 +320,12 @@ gemm_rb_kernel(GemmParams p) {
     auto step_body = [&](uint32_t s, int j) {
         const int wslot = (j + 1) % WP;
         uint32_t (*bn)[16] = bw[(j + 1) & 1];
-        const uint32_t gn = g_begin + (s + 1) * 2 + h;
+        const uint32_t gn = g_begin + (s + KG) * 2 + h;
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             __builtin_amdgcn_sched_barrier(0);
-            if (kk < 3) read_a(j % XS, kk + 1, af[(kk + 1) & 1]);
-            else read_a((j + 1) % XS, 0, af[0]);
+            if (kk < 3) read_a(j, kk + 1, af[(kk + 1) & 1]);
+            else read_a(j + 1, 0, af[0]);
 #pragma unroll
             for (int jb = 0; jb < NCB; jb++) {
                 const uint32_t* bj = bw[j & 1][jb];
@@ -360,7 +373,7 @@ gemm_rb_kernel(GemmParams p) {
                 }
             }
         }
-        load_w(s + 1 + WP, wslot);
+        load_w(s + KG * (1 + WP), wslot);
         __syncthreads();
     };
 
@@ -368,26 +381,59 @@ gemm_rb_kernel(GemmParams p) {
 #pragma unroll
     for (int t = 0; t < XP; t++) load_x(t, t);
 #pragma unroll
-    for (int t = 0; t < WP; t++) load_w(t, t);
+    for (int t = 0; t < WP; t++) load_w(KG * t + kg, t);
     store_x(0, 0);
     store_x(1, 1);
     load_x(XP, 0);
     load_x(XP + 1, 1);
-    decode(0, 0, bw[0]);
-    load_w(WP, 0);
+    decode(kg, 0, bw[0]);
+    load_w(KG * WP + kg, 0);
     __syncthreads();
     read_a(0, 0, af[0]);
 
     // ---- main loop: full groups of U steps branch-free (look-ahead fetches past
     // the K range read zeros), then the remainder with guards ----
-    uint32_t s0 = 0;
-    for (; s0 + U <= nsteps; s0 += U) {
+    // rounds of KG steps: this wave takes step KG t + kg of round t
+    const uint32_t nloc = nsteps / KG;
+    uint32_t t0 = 0;
+    for (; t0 + U <= nloc; t0 += U) {
 #pragma unroll
-        for (int j = 0; j < U; j++) step_body(s0 + j, j);
+        for (int j = 0; j < U; j++) step_body(KG * (t0 + j) + kg, j);
     }
 #pragma unroll
     for (int j = 0; j < U; j++)
-        if (s0 + j < nsteps) step_body(s0 + j, j);
+        if (t0 + j < nloc) step_body(KG * (t0 + j) + kg, j);
+
+    // ---- K groups: group 1 hands its tile to group 0 through LDS (every
+    // wave is past the last step's barrier, so the X stages are free) ----
+    if constexpr (KG > 1) {
+        static_assert(KG == 2, "two K groups");
+        float* const xg = reinterpret_cast<float*>(lds) + wl * (C::ACC * 64);
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < NCB; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        *reinterpret_cast<f4_t*>(xg + (((i * NCB + j) * 4 + q) * 64 + lane) * 4) =
+                            f4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < NCB; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f4_t o = *reinterpret_cast<const f4_t*>(xg + (((i * NCB + j) * 4 + q) * 64 + lane) * 4);
+                    acc[i][j][4 * q] += o.x;
+                    acc[i][j][4 * q + 1] += o.y;
+                    acc[i][j][4 * q + 2] += o.z;
+                    acc[i][j][4 * q + 3] += o.w;
+                }
+    }
 
     // ---- split-K: this split's fp32 partial sums go to the workspace, laid
     // out [split][plane][M][N] (plane 1: the SwiGLU up projection); the
@@ -517,11 +563,15 @@ gemm_rb_kernel(GemmParams p) {
 }
 
 
-template <int F, int TM, int TN, int NW, int WR, bool DUAL>
+template <int F, int TM, int TN, int NW, int WR, int KG, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
-    using C = rb::Cfg<TM, TN, NW, WR, DUAL>;
-    auto kern = p.ksplit > 1 ? gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, kWeightStages, true>
-                             : gemm_rb_kernel<F, TM, TN, NW, WR, DUAL, kWeightStages, false>;
+    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL>;
+    auto kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, false>;
+    if constexpr (KG > 1) {
+        if (p.ksplit > 1 || (p.K / 64) % KG != 0) return hipErrorInvalidValue;  // rb_pick never asks for these
+    } else {
+        if (p.ksplit > 1) kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, true>;
+    }
     const size_t lds = C::LDS_BYTES;
     const uint32_t ntm = (p.M + C::BM - 1) / C::BM;
     uint32_t T = ntm * ((p.N + C::BN - 1) / C::BN);
@@ -541,10 +591,11 @@ static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
     } else if constexpr (F == QUANT_VAR_RATE_AFFINE || F == QUANT_EXL3) {
         return rb_launch_cfg<F, QR_RB_MID, false>(p, st);  // rb_pick's only shape for these formats
     } else {
-        switch (rb_pick(F, p.M, p.N, false)) {
+        switch (rb_pick(F, p.M, p.N, p.K, false)) {
             case 0: return rb_launch_cfg<F, QR_RB_BIG, false>(p, st);
             case 3: return rb_launch_cfg<F, QR_RB_BIG_K, false>(p, st);
             case 4: return rb_launch_cfg<F, QR_RB_MID64, false>(p, st);
+            case 5: return rb_launch_cfg<F, QR_RB_KG, false>(p, st);
             default: return rb_launch_cfg<F, QR_RB_MID, false>(p, st);
         }
     }

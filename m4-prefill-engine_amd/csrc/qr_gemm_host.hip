@@ -132,14 +132,14 @@ static uint32_t tiles_of(const GemmParams& p, const RbShape& d) {
 bool gemm_grouped_ok(const GemmParams& p) {
     if (p.ngroups < 2 || p.ngroups > 3 || p.W2 || p.R) return false;
     // every group must take the shape group 0 takes, and the grid needs no K split
-    const int s0 = rb_pick(p.format, p.M, p.N, false);
+    const int s0 = rb_pick(p.format, p.M, p.N, p.K, false);
     for (uint32_t g = 1; g < p.ngroups; g++)
-        if (rb_pick(p.format, p.M, p.Nx[g - 1], false) != s0) return false;
+        if (rb_pick(p.format, p.M, p.Nx[g - 1], p.K, false) != s0) return false;
     return gemm_pick_ksplit(p) == 1;
 }
 
 uint32_t gemm_pick_ksplit(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.W2 != nullptr));
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.K, p.W2 != nullptr));
     const uint32_t T = tiles_of(p, d);
     // One workgroup fits a CU (its registers), so the grid runs in waves of
     // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
@@ -154,7 +154,7 @@ size_t gemm_workspace_floats(const GemmParams& p, uint32_t ks) {
 }
 
 uint32_t gemm_group_m(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.W2 != nullptr));
+    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.K, p.W2 != nullptr));
     const uint32_t nt_m = (p.M + d.bm - 1) / d.bm;
     return nt_m >= 4 ? 4u : 2u;
 }

@@ -6,8 +6,8 @@
 
 namespace qr {
 
-// Shapes {TM, TN, NW, WR}: NW waves in WR row groups; BM = 32 TM WR,
-// BN = 32 TN NW / WR.
+// Shapes {TM, TN, NW, WR, KG}: NW waves in KG K groups of WR row groups;
+// BM = 32 TM WR, BN = 32 TN NW / (WR KG).
 //   0 (M >= 1024): QR_RB_BIG  (4, 2, 4 -> 128 x 256; Q4_K and ternary:
 //                  QR_RB_BIG_K, 4, 1, 8 -> 128 x 256 with two waves per
 //                  SIMD, whose heavier decode then overlaps the other wave's MFMAs)
@@ -16,14 +16,18 @@ namespace qr {
 //   4 (M <  1024, last 128-row tile at most half full, cheap-decode formats):
 //                  QR_RB_MID64 (2, 1, 4 -> 64 x 128: e.g. M = 129
 //                  computes 192 rows, not 256)
+//   5 (M <= 128, wide N): QR_RB_KG (4, 1, 4, 1, 2 -> 128 x 64: two K groups
+//                  of two column waves take alternate K steps and meet in LDS,
+//                  so 224 workgroups cover M = 128, N = 14336 with no K split)
 //   dual (SwiGLU): 4, 1, 4 -> 128 x 128 outputs (gate + up: 256 weight columns)
-#define QR_RB_BIG 4, 2, 4, 1
-#define QR_RB_BIG_K 4, 1, 8, 1
-#define QR_RB_MID 4, 1, 4, 1
-#define QR_RB_MID64 2, 1, 4, 1
-#define QR_RB_DUAL 4, 1, 4, 1
-template <int TM, int TN, int NW, int WR> struct ShapeOf {
-    static constexpr uint32_t bm = 32 * TM * WR, bn = 32 * TN * (NW / WR);
+#define QR_RB_BIG 4, 2, 4, 1, 1
+#define QR_RB_BIG_K 4, 1, 8, 1, 1
+#define QR_RB_MID 4, 1, 4, 1, 1
+#define QR_RB_MID64 2, 1, 4, 1, 1
+#define QR_RB_KG 4, 1, 4, 1, 2
+#define QR_RB_DUAL 4, 1, 4, 1, 1
+template <int TM, int TN, int NW, int WR, int KG> struct ShapeOf {
+    static constexpr uint32_t bm = 32 * TM * WR, bn = 32 * TN * (NW / (WR * KG));
 };
 struct RbShape {
     uint32_t bm, bn;
@@ -32,11 +36,14 @@ struct RbShape {
 // 256 CUs; when it cannot (N small), 128 x 128 tiles give twice the tiles, so
 // the K split -- whose fp32 partials are M x N x 4 bytes written and read per
 // extra split -- is halved or avoided.
-inline int rb_pick(int format, uint32_t M, uint32_t N, bool dual) {
+inline int rb_pick(int format, uint32_t M, uint32_t N, uint32_t K, bool dual) {
     if (dual) return 2;
     // The 3/5-bit double-rounding formats (no BASELINE configuration) keep
     // one tile shape: fewer instances of their heavy fp64 decode to compile.
     if (format == QUANT_VAR_RATE_AFFINE || format == QUANT_EXL3) return 1;
+    // K groups instead of a K split: one 128-row tile, enough 64-column tiles
+    // for most of the CUs, whole pairs of 64-K steps
+    if (M <= 128 && (N + 63) / 64 >= 192 && K % 128 == 0) return 5;
     if (M >= 1024) {
         // the heavier decodes (Q4_K's fp32 affine, ternary's 2-bit fields) run
         // best as two waves per SIMD, one decoding while the other multiplies
@@ -60,6 +67,7 @@ inline RbShape rb_dims(int s) {
         case 3: return {ShapeOf<QR_RB_BIG_K>::bm, ShapeOf<QR_RB_BIG_K>::bn};
         case 1: return {ShapeOf<QR_RB_MID>::bm, ShapeOf<QR_RB_MID>::bn};
         case 4: return {ShapeOf<QR_RB_MID64>::bm, ShapeOf<QR_RB_MID64>::bn};
+        case 5: return {ShapeOf<QR_RB_KG>::bm, ShapeOf<QR_RB_KG>::bn};
         default: return {ShapeOf<QR_RB_DUAL>::bm, ShapeOf<QR_RB_DUAL>::bn};
     }
 }

@@ -275,6 +275,46 @@ def test_under_filled_grid_shapes(bridge, oracle, fmt, M, K, N):
     np.testing.assert_array_equal(host(Y2).view(np.uint16), host(Y).view(np.uint16))  # deterministic
 
 
+@pytest.mark.parametrize("fmt,M,K,N", [(1, 128, 4096, 12352), (0, 100, 2176, 12300), (2, 128, 2048, 12288),
+                                       (3, 65, 4096, 12352), (8, 127, 2176, 12416)])
+def test_k_group_tiles(bridge, oracle, fmt, M, K, N):
+    """The 128 x 64 tile whose two K groups take alternate 64-K steps and
+    meet in LDS (M <= 128 with at least 192 column tiles): ragged M and N,
+    K with an odd number of step pairs (2176 = 17 pairs), checked against the
+    oracle on a row sample with every column, and deterministic."""
+    X = synth.activations(M, K, 140 + fmt, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 141 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    rows = np.unique(np.r_[0, 1, 31, 32, 63, 64, M - 1])
+    Xs = np.ascontiguousarray(X[rows])
+    tolerance.check_ref(host(Y)[rows], oracle.gemm(fmt, Xs, W, N), what=f"fmt {fmt} {M}x{K}x{N}")
+    Y2 = empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y2, fmt, M, K, N)
+    bridge.synchronize()
+    np.testing.assert_array_equal(host(Y2).view(np.uint16), host(Y).view(np.uint16))
+
+
+def test_k_group_tiles_head_layout_and_residual(bridge, oracle):
+    """The K-group tile's epilogue with the direct-head layout and a residual."""
+    fmt, M, K, H, D = 0, 128, 2048, 192, 64
+    N = H * D
+    X = synth.activations(M, K, 150, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 151)
+    rows = np.array([0, 5, 64, 127])
+    Xs = np.ascontiguousarray(X[rows])
+    Yh = empty16(H, M, D)
+    bridge.dispatch_head_gemm(dev(X), dev(W), Yh, fmt, M, H, D, K)
+    R = synth.activations(M, N, 152)
+    Yr = empty16(M, N)
+    bridge.dispatch_gemm_residual(dev(X), dev(W), dev(R), Yr, fmt, M, K, N)
+    bridge.synchronize()
+    ref_h = oracle.gemm(fmt, Xs, W, N, head_D=D)  # [H, rows, D]
+    tolerance.check_ref(host(Yh)[:, rows, :], ref_h, what="direct-head")
+    tolerance.check_ref(host(Yr)[rows], oracle.gemm(fmt, Xs, W, N, R=np.ascontiguousarray(R[rows])), what="residual")
+
+
 def test_gemm_q4_0_scales_beyond_fast_path(bridge, oracle):
     """Q4_0 scales with |d| > 8188 (-8 d is not finite in binary16): the tiled
     kernel's fused fma(q, d, -8 d) decode cannot form them, so the wave takes
