@@ -604,7 +604,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(head["tflops"] / PEAK_MFMA_TFLOPS, 4), "traffic": traffic,
                      "traffic_note": traffic_note,
-                     "kernel": "gemm_rb_kernel<MLX_4BIT, 4, 1, 4> (128x128 tiles, K split 2) + splitk_reduce_kernel", "hbm_frac": head.get("frac_hbm")},
+                     "kernel": "gemm_rb_kernel<MLX_4BIT, 4, 1, 4, 1, 2> (128x64 tiles, two K groups and a stager wave; one kernel)", "hbm_frac": head.get("frac_hbm")},
         "per_config": per,
     }
     if not a.no_probes:

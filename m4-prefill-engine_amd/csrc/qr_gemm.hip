@@ -53,7 +53,14 @@ constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
 // NW waves as KG K groups of WR row groups x NW / (WR KG) column groups; a
 // wave's tile is 32 TM rows x 32 TN columns.  With KG = 2 the groups take
 // alternate K steps of the whole K range and sum their tiles in LDS at the end.
-template <int TM, int TN, int NW, int WR, int KG, bool DUAL>
+// Whether an instance stages X through a stager wave: one 32-column tile per
+// wave and no SwiGLU pair (the instances that leave registers for the extra
+// wave), except Q4_K's 8-wave tile, whose registers then spill for no gain.
+constexpr bool use_stager(int F, int TN, int NW, bool DUAL) {
+    return !DUAL && TN == 1 && !(F == QUANT_Q4_K && NW == 8);
+}
+
+template <int TM, int TN, int NW, int WR, int KG, bool DUAL, bool STAGER>
 struct Cfg {
     static_assert(NW % (WR * KG) == 0, "whole column groups");
     static constexpr int NT = 64 * NW;
@@ -66,11 +73,10 @@ struct Cfg {
     static constexpr int XCH = BM * kBK / 8;      // 16-byte X chunks per step
     static constexpr int XPT = (XCH + NT - 1) / NT;
     static constexpr int LDS_STAGE = BM * kLdsRow;  // halfs
-    // X staging: with one 32-column tile per wave and no SwiGLU pair (the
-    // instances that leave registers for a fifth wave), an extra stager wave
-    // copies X to LDS (XST: 6 stages, XD steps ahead); otherwise every wave
-    // fetches X into registers and writes it to a 3-stage ring.
-    static constexpr bool XST = !DUAL && TN == 1;
+    // X staging: an extra stager wave copies X to LDS (XST: KG (XD + 1)
+    // stages, XD rounds ahead), or every wave fetches X into registers and
+    // writes it to a 3-stage ring.
+    static constexpr bool XST = STAGER;
     static constexpr int NTL = NT + (XST ? 64 : 0);  // threads per workgroup
     static_assert(KG == 1 || XST, "K groups take X from the stager");
     static constexpr int XD = KG > 1 ? 3 : 5;                // rounds of KG steps the copies run ahead
@@ -122,9 +128,9 @@ __device__ __forceinline__ void rb_wait_vmcnt() {
 }
 
 template <int F, int TM, int TN, int NW, int WR, int KG, bool DUAL, int P, bool SPLIT>
-__global__ void __launch_bounds__(64 * NW + (!DUAL && TN == 1 ? 64 : 0), 1)
+__global__ void __launch_bounds__(64 * NW + (rb::use_stager(F, TN, NW, DUAL) ? 64 : 0), 1)
 gemm_rb_kernel(GemmParams p) {
-    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL>;
+    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, DUAL)>;
     static_assert(!(SPLIT && KG > 1), "K groups replace the K split");
     using Dec = Decoder<F>;
     constexpr int NT = C::NT;
@@ -565,7 +571,7 @@ gemm_rb_kernel(GemmParams p) {
 
 template <int F, int TM, int TN, int NW, int WR, int KG, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
-    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL>;
+    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, DUAL)>;
     auto kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, false>;
     if constexpr (KG > 1) {
         if (p.ksplit > 1 || (p.K / 64) % KG != 0) return hipErrorInvalidValue;  // rb_pick never asks for these
