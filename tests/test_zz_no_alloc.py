@@ -5,7 +5,8 @@ Checked through the C-ABI against m4_bridge_dispatch_gemm on the same inputs,
 bit for bit (both run the same kernels; the split-K sums are taken in split
 order, so the workspace they live in cannot change a bit), on two calls in a
 row -- the second smaller, so stale partials of the first would show -- and at
-the BASELINE shapes that split K (the headline and config 1).
+the BASELINE headline and config 1 (single kernels with no partials: the
+entry point must run them unchanged).
 """
 from __future__ import annotations
 
@@ -35,7 +36,7 @@ def _run(lib, fn, X, W, fmt, M, K, N):
 
 
 @pytest.mark.parametrize("calls", [
-    [(1, 128, 4096, 14336), (0, 33, 4096, 4096)],    # headline (tiled, K split 2), then config 1 (small-M, split)
+    [(1, 128, 4096, 14336), (0, 33, 4096, 4096)],    # headline (K groups), then config 1 (small-M, one kernel)
     [(0, 300, 4096, 384), (2, 65, 2048, 256)],       # tiled split-K shapes, second smaller
     [(3, 48, 4096, 2048), (1, 16, 2048, 512)],       # small-M split-K, second smaller
 ])
