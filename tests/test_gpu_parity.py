@@ -405,6 +405,24 @@ def test_gemm_small_m_wide(bridge, oracle, fmt, M, K, N):
                                       host(Y)[rows].view(np.uint16))
 
 
+@pytest.mark.parametrize("fmt,M,K,N", [(0, 129, 96, 256), (1, 200, 160, 384), (3, 300, 2080, 512),
+                                       (6, 129, 160, 256), (0, 2048, 1056, 512), (3, 129, 4128, 8192)])
+def test_gemm_half_last_step(bridge, oracle, fmt, M, K, N):
+    """K with a half last 64-K step (K % 64 == 32) through the tiled kernel:
+    the stager (or the register path) must copy zeros for the step's upper 32
+    K, and the K split (4128 = 2 x 2064 at cfg4's shape) gives every split a
+    half last step of its own."""
+    X = synth.activations(M, K, 160 + fmt, std=0.35)
+    W = synth.random_blocks(fmt, N, K, 161 + fmt)
+    Y = empty16(M, N)
+    bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
+    bridge.synchronize()
+    rows = np.unique(np.r_[0, 1, 63, 64, 127, 128, M - 1])
+    rows = rows[rows < M]
+    Xs = np.ascontiguousarray(X[rows])
+    tolerance.check_ref(host(Y)[rows], oracle.gemm(fmt, Xs, W, N), what=f"fmt {fmt} {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("fmt", [6, 7])
 @pytest.mark.parametrize("M,K,N", [(1, 384, 256), (33, 384, 200), (129, 512, 256), (128, 4096, 320),
                                    (300, 1152, 136)])
