@@ -410,8 +410,8 @@ def test_gemm_small_m_wide(bridge, oracle, fmt, M, K, N):
 def test_gemm_half_last_step(bridge, oracle, fmt, M, K, N):
     """K with a half last 64-K step (K % 64 == 32) through the tiled kernel:
     the stager (or the register path) must copy zeros for the step's upper 32
-    K, and the K split (4128 = 2 x 2064 at cfg4's shape) gives every split a
-    half last step of its own."""
+    K (a K split needs K to be a multiple of 512, so no split has a half
+    step); 4128 at cfg4's shape, M = 2048 on the two-B-tile instance."""
     X = synth.activations(M, K, 160 + fmt, std=0.35)
     W = synth.random_blocks(fmt, N, K, 161 + fmt)
     Y = empty16(M, N)
