@@ -56,8 +56,8 @@ constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
 // Whether an instance stages X through a stager wave: one 32-column tile per
 // wave and no SwiGLU pair (the instances that leave registers for the extra
 // wave), except Q4_K's 8-wave tile, whose registers then spill for no gain.
-constexpr bool use_stager(int F, int TN, int NW, bool DUAL) {
-    return !DUAL && TN == 1 && !(F == QUANT_Q4_K && NW == 8);
+constexpr bool use_stager(int F, int TN, int NW, int KG, bool DUAL) {
+    return !DUAL && TN == 1 && !(F == QUANT_Q4_K && NW == 8 && KG == 1);
 }
 
 template <int TM, int TN, int NW, int WR, int KG, bool DUAL, bool STAGER>
@@ -128,9 +128,9 @@ __device__ __forceinline__ void rb_wait_vmcnt() {
 }
 
 template <int F, int TM, int TN, int NW, int WR, int KG, bool DUAL, int P, bool SPLIT>
-__global__ void __launch_bounds__(64 * NW + (rb::use_stager(F, TN, NW, DUAL) ? 64 : 0), 1)
+__global__ void __launch_bounds__(64 * NW + (rb::use_stager(F, TN, NW, KG, DUAL) ? 64 : 0), 1)
 gemm_rb_kernel(GemmParams p) {
-    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, DUAL)>;
+    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, KG, DUAL)>;
     static_assert(!(SPLIT && KG > 1), "K groups replace the K split");
     using Dec = Decoder<F>;
     constexpr int NT = C::NT;
@@ -571,7 +571,7 @@ gemm_rb_kernel(GemmParams p) {
 
 template <int F, int TM, int TN, int NW, int WR, int KG, bool DUAL>
 static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
-    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, DUAL)>;
+    using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, KG, DUAL)>;
     auto kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, false>;
     if constexpr (KG > 1) {
         if (p.ksplit > 1 || (p.K / 64) % KG != 0) return hipErrorInvalidValue;  // rb_pick never asks for these
@@ -602,6 +602,7 @@ static hipError_t rb_launch_fmt(const GemmParams& p, hipStream_t st) {
             case 3: return rb_launch_cfg<F, QR_RB_BIG_K, false>(p, st);
             case 4: return rb_launch_cfg<F, QR_RB_MID64, false>(p, st);
             case 5: return rb_launch_cfg<F, QR_RB_KG, false>(p, st);
+            case 6: return rb_launch_cfg<F, QR_RB_MID64_KG, false>(p, st);
             default: return rb_launch_cfg<F, QR_RB_MID, false>(p, st);
         }
     }

@@ -139,7 +139,9 @@ bool gemm_grouped_ok(const GemmParams& p) {
 }
 
 uint32_t gemm_pick_ksplit(const GemmParams& p) {
-    const RbShape d = rb_dims(rb_pick(p.format, p.M, p.N, p.K, p.W2 != nullptr));
+    const int shape = rb_pick(p.format, p.M, p.N, p.K, p.W2 != nullptr);
+    if (shape == 5 || shape == 6) return 1;  // K groups: the tile takes the whole K range
+    const RbShape d = rb_dims(shape);
     const uint32_t T = tiles_of(p, d);
     // One workgroup fits a CU (its registers), so the grid runs in waves of
     // 256 workgroups: split K (powers of two, whole 256-element super-blocks,
