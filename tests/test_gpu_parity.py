@@ -277,10 +277,13 @@ def test_under_filled_grid_shapes(bridge, oracle, fmt, M, K, N):
 
 @pytest.mark.parametrize("fmt,M,K,N", [(1, 128, 4096, 12352), (0, 100, 2176, 12300), (2, 128, 2048, 12288),
                                        (3, 65, 4096, 12352), (8, 127, 2176, 12416), (1, 128, 128, 12288),
-                                       (0, 96, 384, 12352), (0, 40, 4096, 12352)])
+                                       (0, 96, 384, 12352), (0, 40, 4096, 12352),
+                                       (3, 150, 2048, 8200), (0, 129, 1152, 8192), (1, 140, 4096, 16384)])
 def test_k_group_tiles(bridge, oracle, fmt, M, K, N):
     """The 128 x 64 tile whose two K groups take alternate 64-K steps and
-    meet in LDS (M <= 128 with at least 192 column tiles): ragged M and N,
+    meet in LDS (M <= 128 with at least 192 column tiles), and the 64 x 128
+    tile as two K groups (M past a multiple of 128 by at most 64, no K split
+    needed: M = 129, 140, 150): ragged M and N,
     K with an odd number of step pairs (2176 = 17 pairs), one or three pairs
     (K = 128, 384: fewer rounds than the stager runs ahead), M = 40 (whichever
     small-M or tiled path takes it), checked against the oracle on a row
@@ -290,7 +293,7 @@ def test_k_group_tiles(bridge, oracle, fmt, M, K, N):
     Y = empty16(M, N)
     bridge.dispatch_router_gemm(dev(X), dev(W), Y, fmt, M, K, N)
     bridge.synchronize()
-    rows = np.unique(np.r_[0, 1, 31, 32, 63, 64, M - 1])
+    rows = np.unique(np.r_[0, 1, 31, 32, 63, 64, 127, 128, M - 1])
     rows = rows[rows < M]
     Xs = np.ascontiguousarray(X[rows])
     tolerance.check_ref(host(Y)[rows], oracle.gemm(fmt, Xs, W, N), what=f"fmt {fmt} {M}x{K}x{N}")
