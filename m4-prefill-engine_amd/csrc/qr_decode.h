@@ -47,20 +47,28 @@ template <> struct Decoder<QUANT_Q4_0> {
     __device__ static uint32_t scale_bits(const uint32_t raw[5], uint32_t parity2) {
         return parity2 ? (raw[0] >> 16) : (raw[0] & 0xffffu);  // block at byte 2 of raw[0]?
     }
-    __device__ static uint32_t codes(const uint32_t raw[5], uint32_t parity2, int i) {
-        return parity2 ? raw[i + 1] : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
+    // The lane's block starts at byte parity2 (0 or 2) of raw[0]; one byte
+    // permute per word picks the code dword (bytes 2 .. 5, or 4 .. 7, of the
+    // pair raw[i], raw[i + 1]) and the scale twice (d, d), with the selector
+    // formed once per block instead of a select per word.
+    __device__ static uint32_t code_sel(uint32_t parity2) { return 0x05040302u + parity2 * 0x01010101u; }
+    __device__ static uint32_t codes(const uint32_t raw[5], uint32_t sel, int i) {
+        return perm(raw[i + 1], raw[i], sel);
+    }
+    __device__ static uint32_t scale_pair(const uint32_t raw[5], uint32_t sel) {
+        return perm(raw[0], raw[0], sel - 0x04040202u);  // bytes 0 1 0 1 or 2 3 2 3
     }
     // GEMM operand path: fma(q, d, -8 d) -- -8 d is exact and the fused op
     // rounds once.  Valid while -8 d is finite (|d| <= 8188); needs_exact()
     // flags the rest.  Zero weights come out +0 (see above).
     __device__ static void decode_half_fast(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
-        const uint32_t d16 = scale_bits(raw, parity2);
-        const h2_t d = as_h2(d16 | (d16 << 16));
+        const uint32_t sel = code_sel(parity2);
+        const h2_t d = as_h2(scale_pair(raw, sel));
         const h2_t m8 = {(_Float16)-8.0f, (_Float16)-8.0f};
         const h2_t c = d * m8;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t q = codes(raw, parity2, i);
+            const uint32_t q = codes(raw, sel, i);
             const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
             out[2 * i + 0] = as_u32(__builtin_elementwise_fma(code_pair<false>(n), d, c));
             out[2 * i + 1] = as_u32(__builtin_elementwise_fma(code_pair<true>(n), d, c));
@@ -68,12 +76,12 @@ template <> struct Decoder<QUANT_Q4_0> {
     }
     // Any scale: (q - 8) exact in binary16, one rounding in the product.
     __device__ static void decode_half_exact(const uint32_t raw[5], uint32_t parity2, int h, uint32_t out[8]) {
-        const uint32_t d16 = scale_bits(raw, parity2);
-        const h2_t d = as_h2(d16 | (d16 << 16));
+        const uint32_t sel = code_sel(parity2);
+        const h2_t d = as_h2(scale_pair(raw, sel));
         const h2_t off = {(_Float16)8.0f, (_Float16)8.0f};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t q = codes(raw, parity2, i);
+            const uint32_t q = codes(raw, sel, i);
             const uint32_t n = (h ? (q >> 4) : q) & 0x0f0f0f0fu;
             out[2 * i + 0] = as_u32((code_pair<false>(n) - off) * d);
             out[2 * i + 1] = as_u32((code_pair<true>(n) - off) * d);
