@@ -69,6 +69,14 @@ __device__ __forceinline__ uint32_t rne16_sum(float p, float q) {
 }
 
 // Byte permute: D.byte[i] = sel.byte[i] in 0..3 -> s1.byte, 4..7 -> s0.byte, 0x0c -> 0.
+// SiLU(g) * u in fp32 for the SwiGLU epilogues: g / (1 + e^-g) through the
+// hardware reciprocal (about 1 ulp of fp32, far inside the fp16 result's
+// rounding) instead of an IEEE division sequence; e^-g = inf gives -0 and
+// e^-g = 0 gives g, as the division does.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
     return __builtin_amdgcn_perm(s0, s1, sel);
 }

@@ -476,7 +476,7 @@ gemm_rb_kernel(GemmParams p) {
         float v = acc[i][j][r];
         if constexpr (DUAL) {
             const float u = acc[i][j + TN][r];
-            v = v / (1.0f + __expf(-v)) * u;
+            v = silu_mul(v, u);
         }
         return v;
     };

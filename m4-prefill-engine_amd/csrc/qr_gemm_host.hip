@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
 #pragma unroll
         for (int q = 0; q < kRedVec; q++) {
             v[q] = g[q];
-            if constexpr (DUAL) v[q] = v[q] / (1.0f + __expf(-v[q])) * u[q];
+            if constexpr (DUAL) v[q] = silu_mul(v[q], u[q]);
         }
         if (R) {
             const u4_t rr = *reinterpret_cast<const u4_t*>(R + e0);
@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
         const size_t e = e0 + q;
         const uint32_t m = (uint32_t)(e / N), n = (uint32_t)(e % N);
         float v = g[q];
-        if constexpr (DUAL) v = v / (1.0f + __expf(-v)) * u[q];
+        if constexpr (DUAL) v = silu_mul(v, u[q]);
         if (R) v += (float)R[e];
         const size_t o = head_D ? ((size_t)(n / head_D) * M + m) * head_D + n % head_D : e;
         Y[o] = (_Float16)v;
