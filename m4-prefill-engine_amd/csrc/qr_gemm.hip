@@ -72,7 +72,13 @@ struct Cfg {
     static constexpr int NCB = DUAL ? 2 * TN : TN;  // 32-column B tiles per wave (gate, then up)
     static constexpr int XCH = BM * kBK / 8;      // 16-byte X chunks per step
     static constexpr int XPT = (XCH + NT - 1) / NT;
-    static constexpr int LDS_STAGE = BM * kLdsRow;  // halfs
+    // stager stages: unpadded, XOR-swizzled rows (the lane's 4 TM read offsets
+    // held in registers), except where two 128-row waves per SIMD leave no
+    // registers for them (the 8-wave 128 x 256 tile then spills: ternary at
+    // M = 2048 80 vs 69 us); there the rows keep their pad unit
+    static constexpr bool XSW = STAGER && (NW == 4 || TM <= 2);
+    static constexpr int XROW = XSW ? kBK : kLdsRow;  // halfs per LDS row of an X stage
+    static constexpr int LDS_STAGE = BM * XROW;   // halfs
     // X staging: an extra stager wave copies X to LDS (XST: KG (XD + 1)
     // stages, XD rounds ahead), or every wave fetches X into registers and
     // writes it to a 3-stage ring.
@@ -82,7 +88,7 @@ struct Cfg {
     static constexpr int XD = KG > 1 ? 3 : 5;                // rounds of KG steps the copies run ahead
     static constexpr int XS = XST ? KG * (XD + 1) : 3;       // X stages in LDS
     static constexpr int U = KG > 1 ? 4 : 6;                 // rounds unrolled (ring indices static)
-    static constexpr int XCP = BM * (kLdsRow / 8) / 64;  // 64-lane copies per stage (pad units included)
+    static constexpr int XCP = BM * (XROW / 8) / 64;  // 64-lane copies per stage
     static constexpr int ACC = TM * NCB * 16;     // accumulator floats per lane
     // Epilogue staging (floats): the 32-column tile j of a wave row starts at
     // column EJS * j and rows are ERS apart.  The compiler pairs the band's
@@ -97,6 +103,12 @@ struct Cfg {
     static constexpr int LDS_BYTES0 = XS * LDS_STAGE * 2 > EPI_BYTES ? XS * LDS_STAGE * 2 : EPI_BYTES;
     static constexpr int LDS_BYTES = LDS_BYTES0 > XCH_BYTES ? LDS_BYTES0 : XCH_BYTES;
 };
+
+// Swizzle of the stager's unpadded 128-byte X rows: logical 16-byte unit c of
+// row r sits at unit c ^ xswz(r).  The 8 rows of one ds_read_b128 pass (and
+// the 16 rows of a pass that serves 16 lanes from 64 banks: rows of one parity
+// take the even or the odd values) hit distinct bank groups.
+__device__ __forceinline__ uint32_t xswz(uint32_t r) { return (r ^ (r >> 3)) & 7u; }
 
 __device__ __forceinline__ void tile_of(uint32_t bid, uint32_t nt_m, uint32_t nt_n, uint32_t gm_req, uint32_t& tm,
                                         uint32_t& tn) {
@@ -179,8 +191,9 @@ gemm_rb_kernel(GemmParams p) {
     const int ncols = min(C::BN, (int)N - n0);
     auto xr = make_rsrc(p.X + (size_t)m0 * K, (uint32_t)mrows * K * 2u);
     // ---- X stager (XST): the extra wave NW copies each step's BM x 64 slice of X
-    // into an LDS stage (rows of kLdsRow halfs: 8 16-byte units and a pad
-    // unit, copied as zeros) by buffer-load-to-LDS, XD steps ahead, through
+    // into an LDS stage (XSW: 128-byte rows, units XOR-swizzled; else rows of
+    // kLdsRow halfs: 8 16-byte units and a pad unit, copied as zeros) by
+    // buffer-load-to-LDS, XD steps ahead, through
     // a ring of XS stages; the compute waves never touch X in memory.  Before
     // the barrier that opens step t it waits (its own copies, in order) for
     // the copies of step t + 1, whose first k-slice the compute waves read
@@ -189,13 +202,23 @@ gemm_rb_kernel(GemmParams p) {
     // holds barriers).  With K groups a round is KG consecutive steps, one
     // per group, and the same holds per round. ----
     if (C::XST && wave == NW) {
-        constexpr int UPR = kLdsRow / 8;  // 16-byte units per LDS row
         uint32_t xo[C::XCP], xh[C::XCP];  // per-lane offsets: whole step, first half (a 32-K last step)
 #pragma unroll
         for (int q = 0; q < C::XCP; q++) {
-            const uint32_t u = 64u * q + lane, row = u / UPR, cu = u % UPR;
-            const bool live = cu < 8 && row < (uint32_t)mrows;
-            xo[q] = live ? (row * K + 8u * cu) * 2u : kOOB;
+            uint32_t row, cu;
+            bool live;
+            if constexpr (C::XSW) {  // LDS unit pu of a row holds logical unit pu ^ xswz(row)
+                const uint32_t u = 64u * q + lane;
+                row = u / 8u;
+                cu = (u % 8u) ^ rb::xswz(row);
+                live = true;
+            } else {  // 9 units per row, the ninth a pad copied as zeros
+                const uint32_t u = 64u * q + lane;
+                row = u / 9u;
+                cu = u % 9u;
+                live = cu < 8;
+            }
+            xo[q] = live && row < (uint32_t)mrows ? (row * K + 8u * cu) * 2u : kOOB;
             xh[q] = cu < 4 ? xo[q] : kOOB;
         }
         auto issue = [&](uint32_t t) {
@@ -303,12 +326,27 @@ gemm_rb_kernel(GemmParams p) {
 
     const int arow = wrow * C::WM + c32;
     const int akof = 32 * h;
+    // swizzled stages: the lane's offset (halfs) of row tile i, k-slice kk
+    uint32_t aswz[C::XSW ? TM : 1][4];
+    if constexpr (C::XSW) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const uint32_t r = (uint32_t)(arow + i * 32);
+                aswz[i][kk] = r * kBK + 8u * ((4u * (uint32_t)h + (uint32_t)kk) ^ rb::xswz(r));
+            }
+    }
     // stage of local round j (static within the unroll) plus the K group
     auto read_a = [&](int j, int kk, h8_t out[TM]) {
         const _Float16* As = lds + ((KG * j) % XS + kg) * C::LDS_STAGE;
 #pragma unroll
-        for (int i = 0; i < TM; i++)
-            out[i] = *reinterpret_cast<const h8_t*>(As + (arow + i * 32) * kLdsRow + akof + kk * 8);
+        for (int i = 0; i < TM; i++) {
+            if constexpr (C::XSW)
+                out[i] = *reinterpret_cast<const h8_t*>(As + aswz[i][kk]);
+            else
+                out[i] = *reinterpret_cast<const h8_t*>(As + (arow + i * 32) * kLdsRow + akof + kk * 8);
+        }
     };
 
     uint32_t bw[2][NCB][16];
