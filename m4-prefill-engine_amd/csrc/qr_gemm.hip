@@ -50,9 +50,6 @@ namespace rb {
 constexpr int kBK = 64;
 constexpr int kLdsRow = kBK + 8;  // halfs per LDS row of the X stage
 
-// NW waves as KG K groups of WR row groups x NW / (WR KG) column groups; a
-// wave's tile is 32 TM rows x 32 TN columns.  With KG = 2 the groups take
-// alternate K steps of the whole K range and sum their tiles in LDS at the end.
 // Whether an instance stages X through a stager wave: one 32-column tile per
 // wave and no SwiGLU pair (the instances that leave registers for the extra
 // wave), except Q4_K's 8-wave tile, whose registers then spill for no gain.
@@ -60,6 +57,9 @@ constexpr bool use_stager(int F, int TN, int NW, int KG, bool DUAL) {
     return !DUAL && TN == 1 && !(F == QUANT_Q4_K && NW == 8 && KG == 1);
 }
 
+// NW waves as KG K groups of WR row groups x NW / (WR KG) column groups; a
+// wave's tile is 32 TM rows x 32 TN columns.  With KG = 2 the groups take
+// alternate K steps of the whole K range and sum their tiles in LDS at the end.
 template <int TM, int TN, int NW, int WR, int KG, bool DUAL, bool STAGER>
 struct Cfg {
     static_assert(NW % (WR * KG) == 0, "whole column groups");
@@ -99,9 +99,9 @@ struct Cfg {
     static constexpr int EJS = TN > 1 ? 48 : 32;
     static constexpr int ERS = TN > 1 ? (EJS * (TN - 1) + 32 + 31) / 32 * 32 : 48;
     static constexpr int EPI_BYTES = NW * 32 * ERS * 4;
-    static constexpr int XCH_BYTES = KG > 1 ? NW / KG * ACC * 64 * 4 : 0;  // K-group exchange
+    static constexpr int KGX_BYTES = KG > 1 ? NW / KG * ACC * 64 * 4 : 0;  // K-group exchange
     static constexpr int LDS_BYTES0 = XS * LDS_STAGE * 2 > EPI_BYTES ? XS * LDS_STAGE * 2 : EPI_BYTES;
-    static constexpr int LDS_BYTES = LDS_BYTES0 > XCH_BYTES ? LDS_BYTES0 : XCH_BYTES;
+    static constexpr int LDS_BYTES = LDS_BYTES0 > KGX_BYTES ? LDS_BYTES0 : KGX_BYTES;
 };
 
 // Swizzle of the stager's unpadded 128-byte X rows: logical 16-byte unit c of
