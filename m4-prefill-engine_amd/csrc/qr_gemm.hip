@@ -57,6 +57,18 @@ constexpr bool use_stager(int F, int TN, int NW, int KG, bool DUAL) {
     return !DUAL && TN == 1 && !(F == QUANT_Q4_K && NW == 8 && KG == 1);
 }
 
+// Weights through the stager too (WST): the K-group tiles with MLX blocks
+// (20 bytes per group: one round of two 64-K steps is 80 bytes, 5 whole
+// 16-byte units, per column).  The stager copies each round's weights into a
+// 4-stage LDS ring ahead of the round's X; the compute waves read their raw
+// words from LDS just before decoding instead of fetching them (headline
+// 32.1 -> 31.3 us over four rounds).
+constexpr bool use_wstage(int F, int KG, bool stager) {
+    return stager && KG == 2 && F == QUANT_MLX_4BIT;
+}
+constexpr int kWRoundBytes = 80;  // one column's weights of one round (MLX)
+constexpr int kWStages = 4;
+
 // NW waves as KG K groups of WR row groups x NW / (WR KG) column groups; a
 // wave's tile is 32 TM rows x 32 TN columns.  With KG = 2 the groups take
 // alternate K steps of the whole K range and sum their tiles in LDS at the end.
@@ -144,6 +156,10 @@ __global__ void __launch_bounds__(64 * NW + (rb::use_stager(F, TN, NW, KG, DUAL)
 gemm_rb_kernel(GemmParams p) {
     using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, KG, DUAL)>;
     static_assert(!(SPLIT && KG > 1), "K groups replace the K split");
+    constexpr bool WST = rb::use_wstage(F, KG, C::XST);
+    constexpr int WRING = WST ? rb::kWStages * C::BN * rb::kWRoundBytes : 0;  // bytes
+    constexpr int XBYTES = C::XS * C::LDS_STAGE * 2;                           // X stages (bytes)
+    static_assert(!WST || C::BN * rb::kWRoundBytes % 1024 == 0, "whole 1 KB weight copies per round");
     using Dec = Decoder<F>;
     constexpr int NT = C::NT;
     constexpr int NCB = C::NCB;
@@ -221,7 +237,30 @@ gemm_rb_kernel(GemmParams p) {
             xo[q] = live && row < (uint32_t)mrows ? (row * K + 8u * cu) * 2u : kOOB;
             xh[q] = cu < 4 ? xo[q] : kOOB;
         }
+        // weight copies of a round (WST): LDS unit u = col * 5 + unit of the
+        // stage, copy c covering units 64 c .. 64 c + 63
+        constexpr int WCP = WST ? C::BN * rb::kWRoundBytes / 1024 : 0;
+        const auto wsr = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
+        uint32_t wo[WCP ? WCP : 1];
+#pragma unroll
+        for (int c = 0; c < WCP; c++) {
+            const uint32_t u = 64u * c + lane, col = u / 5u, unit = u % 5u;
+            wo[c] = col < (uint32_t)ncols ? col * col_bytes + 16u * unit : kOOB;
+        }
         auto issue = [&](uint32_t t) {
+            if constexpr (WST) {
+                if (t % KG == 0) {  // the round's weights ahead of its X
+                    const uint32_t q = t / KG;
+                    const uint32_t wsoff = (g_begin + 4u * q) * 20u;
+                    uint8_t* const wdst = reinterpret_cast<uint8_t*>(lds) + XBYTES + (q % rb::kWStages) * (C::BN * rb::kWRoundBytes);
+#pragma unroll
+                    for (int c = 0; c < WCP; c++) {
+                        const uint32_t vo = wo[c];
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (__attribute__((address_space(3))) void*)(wdst + c * 1024),
+                                                                 16, vo, (int)wsoff, 0, 0);
+                    }
+                }
+            }
             const uint32_t soff = (k_begin + t * kBK) * 2u;
             const bool half = k_begin + t * kBK + kBK > k_end;
             _Float16* const dst = lds + (t % C::XS) * C::LDS_STAGE;
@@ -238,10 +277,15 @@ gemm_rb_kernel(GemmParams p) {
             // the barrier opening round t needs steps .. KG (t + 2) - 1; copies
             // issued after those: steps KG (t + 2) .. min(KG (t + XD) - 1, nsteps - 1)
             const int r = min(KG * (C::XD - 2), (int)nsteps - KG * ((int)t + 2));
-            if (r >= 3) rb_wait_vmcnt<3 * C::XCP>();
-            else if (r == 2) rb_wait_vmcnt<2 * C::XCP>();
-            else if (r == 1) rb_wait_vmcnt<C::XCP>();
-            else rb_wait_vmcnt<0>();
+            if constexpr (WST) {  // whole rounds: their weight copies, then their X
+                if (r >= KG) rb_wait_vmcnt<KG * C::XCP + WCP>();
+                else rb_wait_vmcnt<0>();
+            } else {
+                if (r >= 3) rb_wait_vmcnt<3 * C::XCP>();
+                else if (r == 2) rb_wait_vmcnt<2 * C::XCP>();
+                else if (r == 1) rb_wait_vmcnt<C::XCP>();
+                else rb_wait_vmcnt<0>();
+            }
             asm volatile("s_barrier" ::: "memory");
 #pragma unroll
             for (int i = 0; i < KG; i++)
@@ -250,6 +294,7 @@ gemm_rb_kernel(GemmParams p) {
         return;
     }
     static_assert(!C::XST || (KG * (C::XD - 2) <= 3 && 3 * C::XCP < 64), "stager waits");
+    static_assert(!WST || (C::XD - 2 == 1 && KG * C::XCP + C::BN * rb::kWRoundBytes / 1024 < 64), "stager waits (WST)");
     auto wr0 = make_rsrc(p.W + (size_t)n0 * col_bytes, (uint32_t)ncols * col_bytes);
     auto wr1 = make_rsrc(DUAL ? p.W2 + (size_t)n0 * col_bytes : p.W, DUAL ? (uint32_t)ncols * col_bytes : 0u);
 
@@ -284,7 +329,18 @@ gemm_rb_kernel(GemmParams p) {
             }
         }
     };
+    // WST: the raw words of this lane's group of local round jr + 1's step
+    auto read_w = [&](int jr, int slot) {
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(lds) + XBYTES + (jr % rb::kWStages) * (C::BN * rb::kWRoundBytes) +
+                              (2 * kg + h) * 20;
+#pragma unroll
+        for (int jb = 0; jb < NCB; jb++)
+#pragma unroll
+            for (int i = 0; i < Dec::kRawWords; i++)
+                wraw[slot][jb][i] = *reinterpret_cast<const uint32_t*>(base + bcol(jb) * rb::kWRoundBytes + 4 * i);
+    };
     auto load_w = [&](uint32_t step, int slot) {
+        if constexpr (WST) return;
         const uint32_t g = g_begin + step * 2 + h;
         const bool live = g < g_end;
 #pragma unroll
@@ -363,6 +419,7 @@ gemm_rb_kernel(GemmParams p) {
     constexpr int DPS = (HALVES + 3) / 4;   // half-group decodes per slice
     auto step_body = [&](uint32_t s, int j) {
         const int wslot = (j + 1) % WP;
+        if constexpr (WST) read_w(j + 1, wslot);  // the next round's weights (visible since this round's barrier)
         uint32_t (*bn)[16] = bw[(j + 1) & 1];
         const uint32_t gn = g_begin + (s + KG) * 2 + h;
 #pragma unroll
@@ -430,9 +487,15 @@ gemm_rb_kernel(GemmParams p) {
     store_x(1, 1);
     load_x(XP, 0);
     load_x(XP + 1, 1);
-    decode(kg, 0, bw[0]);
-    load_w(KG * WP + kg, 0);
-    __syncthreads();
+    if constexpr (WST) {
+        __syncthreads();
+        read_w(0, 0);
+        decode(kg, 0, bw[0]);
+    } else {
+        decode(kg, 0, bw[0]);
+        load_w(KG * WP + kg, 0);
+        __syncthreads();
+    }
     read_a(0, 0, af[0]);
 
     // ---- main loop: full groups of U steps branch-free (look-ahead fetches past
@@ -616,7 +679,9 @@ static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     } else {
         if (p.ksplit > 1) kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, true>;
     }
-    const size_t lds = C::LDS_BYTES;
+    constexpr bool WST = rb::use_wstage(F, KG, C::XST);
+    constexpr size_t LX = (size_t)C::XS * C::LDS_STAGE * 2 + (WST ? rb::kWStages * C::BN * rb::kWRoundBytes : 0);
+    const size_t lds = LX > (size_t)C::LDS_BYTES ? LX : (size_t)C::LDS_BYTES;
     const uint32_t ntm = (p.M + C::BM - 1) / C::BM;
     uint32_t T = ntm * ((p.N + C::BN - 1) / C::BN);
     for (uint32_t g = 1; g < p.ngroups && g < 3; g++) T += ntm * ((p.Nx[g - 1] + C::BN - 1) / C::BN);
