@@ -203,11 +203,16 @@ template <> struct Decoder<QUANT_Q4_K> {
 };
 
 // 16 two-bit codes of word q (element e at bits 2e, LSB first) as 8 binary16
-// pairs (c - 1) d: 1024 + c - 1025 is exact, and so is the product (c - 1) d
-// for c in 0..3 (code 3 gives +2d).  Shared by TERNARY_1_58 and PRISM_Q2_0.
+// pairs (c - 1) d, code 3 giving +2d.  The four values are formed once, as
+// the binary16 products {-1, 0} d and {1, 2} d (exact but for the overflow
+// of 2d, which the CPU gold shares); each pair is then one byte-permute
+// lookup into those 8 bytes, its selector (bytes 2c, 2c + 1 per element)
+// built from the codes by one permute and one shift-or.  Shared by
+// TERNARY_1_58 and PRISM_Q2_0.
 __device__ __forceinline__ void two_bit_word(uint32_t q, uint32_t d16, uint32_t out[8]) {
     const h2_t d = as_h2(d16 | (d16 << 16));
-    const h2_t off = {(_Float16)1025.0f, (_Float16)1025.0f};
+    const uint32_t t01 = as_u32(h2_t{(_Float16)-1.0f, (_Float16)0.0f} * d);  // bytes 0-3: codes 0, 1
+    const uint32_t t23 = as_u32(h2_t{(_Float16)1.0f, (_Float16)2.0f} * d);   // bytes 4-7: codes 2, 3
     const uint32_t ev = q & 0x33333333u;         // codes of even elements, one per nibble
     const uint32_t od = (q >> 2) & 0x33333333u;  // codes of odd elements
     const uint32_t ev_lo = ev & 0x0f0f0f0fu, ev_hi = (ev >> 4) & 0x0f0f0f0fu;
@@ -215,17 +220,17 @@ __device__ __forceinline__ void two_bit_word(uint32_t q, uint32_t d16, uint32_t 
     // nibble j (elements 2j, 2j+1): j even -> byte j/2 of *_lo, j odd -> of *_hi
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-        const uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)(b + 4) << 16);
-        const uint32_t p0 = perm(od_lo, ev_lo, sel) | 0x64006400u;  // nibble 2b
-        const uint32_t p1 = perm(od_hi, ev_hi, sel) | 0x64006400u;  // nibble 2b+1
-        out[2 * b + 0] = as_u32((as_h2(p0) - off) * d);
-        out[2 * b + 1] = as_u32((as_h2(p1) - off) * d);
+        const uint32_t sel = 0x04040000u + 0x01010101u * (uint32_t)b;  // bytes {c_even, c_even, c_odd, c_odd}
+        const uint32_t s0 = (perm(od_lo, ev_lo, sel) << 1) | 0x01000100u;  // nibble 2b
+        const uint32_t s1 = (perm(od_hi, ev_hi, sel) << 1) | 0x01000100u;  // nibble 2b+1
+        out[2 * b + 0] = perm(t23, t01, s0);
+        out[2 * b + 1] = perm(t23, t01, s1);
     }
 }
 
 // --------------------------------------------------------------------------
 // TERNARY_1_58: 12-byte blocks (dword aligned); qs[0] holds elements 0..15,
-// qs[1] elements 16..31, two bits each, LSB first.  w = (1024 + c - 1025) * d
+// qs[1] elements 16..31, two bits each, LSB first.  w = (c - 1) d
 // in binary16: exact for every code, code 3 giving +2d as the CPU gold does.
 // --------------------------------------------------------------------------
 template <> struct Decoder<QUANT_TERNARY_1_58> {
