@@ -269,8 +269,11 @@ gemm_rb_kernel(GemmParams p) {
                 }
             }
             const uint32_t soff = (k_begin + t * kBK) * 2u;
-            const bool half = k_begin + t * kBK + kBK > k_end;
             _Float16* const dst = lds + (t % C::XS) * C::LDS_STAGE;
+            // a 32-K last step (K % 64 == 32) takes the first-half offsets
+            // (K groups take whole 128-K rounds: never, so no per-copy select
+            // and its wait state sit between their copies)
+            const bool half = KG == 1 && k_begin + t * kBK + kBK > k_end;
 #pragma unroll
             for (int q = 0; q < C::XCP; q++) {
                 const uint32_t vo = half ? xh[q] : xo[q];
@@ -682,7 +685,7 @@ static hipError_t rb_launch_cfg(const GemmParams& p, hipStream_t st) {
     using C = rb::Cfg<TM, TN, NW, WR, KG, DUAL, rb::use_stager(F, TN, NW, KG, DUAL)>;
     auto kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, false>;
     if constexpr (KG > 1) {
-        if (p.ksplit > 1 || (p.K / 64) % KG != 0) return hipErrorInvalidValue;  // rb_pick never asks for these
+        if (p.ksplit > 1 || p.K % (64 * KG) != 0) return hipErrorInvalidValue;  // rb_pick never asks for these
     } else {
         if (p.ksplit > 1) kern = gemm_rb_kernel<F, TM, TN, NW, WR, KG, DUAL, kWeightStages, true>;
     }
