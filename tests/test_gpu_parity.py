@@ -278,7 +278,8 @@ def test_under_filled_grid_shapes(bridge, oracle, fmt, M, K, N):
 @pytest.mark.parametrize("fmt,M,K,N", [(1, 128, 4096, 12352), (0, 100, 2176, 12300), (2, 128, 2048, 12288),
                                        (3, 65, 4096, 12352), (8, 127, 2176, 12416), (1, 128, 128, 12288),
                                        (0, 96, 384, 12352), (0, 40, 4096, 12352),
-                                       (3, 150, 2048, 8200), (0, 129, 1152, 8192), (1, 140, 4096, 16384)])
+                                       (3, 150, 2048, 8200), (0, 129, 1152, 8192), (1, 140, 4096, 16384),
+                                       (1, 128, 4160, 12352)])
 def test_k_group_tiles(bridge, oracle, fmt, M, K, N):
     """The 128 x 64 tile whose two K groups take alternate 64-K steps and
     meet in LDS (M <= 128 with at least 192 column tiles), and the 64 x 128
@@ -286,8 +287,9 @@ def test_k_group_tiles(bridge, oracle, fmt, M, K, N):
     needed: M = 129, 140, 150): ragged M and N,
     K with an odd number of step pairs (2176 = 17 pairs), one or three pairs
     (K = 128, 384: fewer rounds than the stager runs ahead), M = 40 (whichever
-    small-M or tiled path takes it), checked against the oracle on a row
-    sample with every column, and deterministic."""
+    small-M or tiled path takes it), K = 4160 (not whole 128-K rounds: the
+    shape choice leaves the K-group tiles), checked against the oracle on a
+    row sample with every column, and deterministic."""
     X = synth.activations(M, K, 140 + fmt, std=0.35)
     W = synth.random_blocks(fmt, N, K, 141 + fmt)
     Y = empty16(M, N)
